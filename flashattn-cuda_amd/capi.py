@@ -1,0 +1,65 @@
+"""ctypes view of the C ABI (include/fa_mi355x.h, include/fa_probe.h).
+
+This is the binding a non-torch host would use: plain pointers, sizes and a
+hipStream_t as an integer. ``load()`` maps libfa_mi355x.so and declares every
+exported signature; ``HEADER_SYMBOLS`` lists the functions the headers declare.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import re
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libfa_mi355x.so"
+INCLUDE = _HERE.parent / "include"
+
+_vp, _i64, _i32p, _fp = C.c_void_p, C.c_int64, C.POINTER(C.c_int32), C.POINTER(C.c_float)
+
+SIGNATURES = {
+    "fa_status_str": (C.c_char_p, [C.c_int]),
+    "fa_abi_version": (C.c_int, []),
+    "fa_validate_fwd": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64]),
+    "fa_fwd_f16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_int, _vp]),
+    "fa_validate_decode": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                     _i64, _i64]),
+    "fa_decode_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
+    "fa_decode_split_f16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                      _i64, _i64, _vp, _vp, _vp]),
+    "fa_lse_combine_f32": (C.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "fa_decode_paged_f16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                      _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "fa_probe_mfma32": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp]),
+    "fa_probe_mfma16": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp]),
+    "fa_probe_tr16_raw": (C.c_int, [_vp, _vp, _vp]),
+    "fa_probe_frags": (C.c_int, [_vp, _vp, _vp, _i64, _vp]),
+    "fa_probe_chain": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
+}
+
+STATUS = {
+    "FA_OK": 0, "FA_ERR_NULL_POINTER": 1, "FA_ERR_HEAD_DIM": 2, "FA_ERR_SEQ_LEN": 3,
+    "FA_ERR_BATCH_HEADS": 4, "FA_ERR_ALIGNMENT": 5, "FA_ERR_TOO_LARGE": 6,
+    "FA_ERR_PAGE_SIZE": 7, "FA_ERR_NUM_SPLITS": 8, "FA_ERR_MAX_PAGES": 9,
+    "FA_ERR_NUM_PAGES": 10,
+}
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/*.h."""
+    names = []
+    for h in sorted(INCLUDE.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(fa_[a-z0-9_]+)\s*\(", text):
+            if m.group(1) not in names:
+                names.append(m.group(1))
+    return names
+
+
+def load(path: pathlib.Path | str = LIB_PATH) -> C.CDLL:
+    """Map the library and declare argument/return types of every C-ABI function."""
+    lib = C.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib

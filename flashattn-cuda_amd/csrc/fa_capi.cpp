@@ -1,0 +1,84 @@
+// fa_capi.cpp — host-only part of the C ABI: argument validation and status
+// strings. No HIP call is made here, so every error path runs without a GPU.
+//
+// fa_validate_fwd mirrors the argument checks of the reference launcher
+// fa3db_full_forward_impl (cuda/flash_attn_fa3_db_full.cu:352-363): head dim,
+// N > 0, and the B*H grid limit, widened to D in {64, 128}; shape/device
+// equality of Q/K/V is the binding's job because the C ABI only sees
+// pointers.
+#include <stdint.h>
+
+#include "fa_mi355x.h"
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Largest element count the kernels index with 32-bit in-head offsets.
+constexpr int64_t kMaxHeadElems = (int64_t(1) << 31) - 1;
+constexpr int64_t kMaxGrid = (int64_t(1) << 31) - 1;
+
+}  // namespace
+
+extern "C" const char* fa_status_str(int status) {
+  switch (status) {
+    case FA_OK: return "ok";
+    case FA_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case FA_ERR_HEAD_DIM: return "Head dimension must be 64 or 128";
+    case FA_ERR_SEQ_LEN: return "N must be > 0";
+    case FA_ERR_BATCH_HEADS: return "B and H must be > 0";
+    case FA_ERR_ALIGNMENT: return "tensor pointers must be 16-byte aligned";
+    case FA_ERR_TOO_LARGE: return "size exceeds the kernels' 32-bit index range";
+    case FA_ERR_PAGE_SIZE: return "page_size must be 16";
+    case FA_ERR_NUM_SPLITS: return "num_splits must be in [1, 16]";
+    case FA_ERR_MAX_PAGES: return "max_pages must be > 0";
+    case FA_ERR_NUM_PAGES: return "num_pages must be > 0";
+    default: break;
+  }
+  if (status < 0) return "HIP error (negated hipError_t)";
+  return "unknown fa_mi355x status";
+}
+
+extern "C" int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+extern "C" int fa_validate_fwd(const void* q, const void* k, const void* v, const void* o,
+                               int64_t B, int64_t H, int64_t N, int64_t D) {
+  if (!q || !k || !v || !o) return FA_ERR_NULL_POINTER;
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (N <= 0) return FA_ERR_SEQ_LEN;
+  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return FA_ERR_ALIGNMENT;
+  if (N * D > kMaxHeadElems) return FA_ERR_TOO_LARGE;
+  if (B > kMaxGrid / H) return FA_ERR_TOO_LARGE;
+  const int64_t bh = B * H;
+  const int64_t num_qb = (N + 127) / 128;
+  if (bh > kMaxGrid / num_qb) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+extern "C" int fa_validate_decode(const void* q, const void* k_pool, const void* v_pool,
+                                  const int32_t* page_table, const int32_t* ctx_lens,
+                                  int64_t B, int64_t H, int64_t D, int64_t page_size,
+                                  int64_t max_pages, int64_t num_pages, int64_t num_splits) {
+  if (!q || !k_pool || !v_pool || !page_table || !ctx_lens) return FA_ERR_NULL_POINTER;
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
+  if (page_size != 16) return FA_ERR_PAGE_SIZE;
+  if (num_splits < 1 || num_splits > 16) return FA_ERR_NUM_SPLITS;
+  if (max_pages <= 0) return FA_ERR_MAX_PAGES;
+  if (num_pages <= 0) return FA_ERR_NUM_PAGES;
+  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool)) return FA_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(page_table) & 3u) || (reinterpret_cast<uintptr_t>(ctx_lens) & 3u))
+    return FA_ERR_ALIGNMENT;
+  // Grid is (num_splits, H, B); y and z are limited to 65535 on this target.
+  if (H > 65535 || B > 65535) return FA_ERR_TOO_LARGE;
+  if (B > kMaxHeadElems / max_pages) return FA_ERR_TOO_LARGE;
+  if (max_pages > kMaxHeadElems / page_size) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+extern "C" int64_t fa_decode_workspace_floats(int64_t B, int64_t H, int64_t D,
+                                              int64_t num_splits) {
+  if (B <= 0 || H <= 0 || D <= 0 || num_splits <= 0) return 0;
+  return B * H * num_splits * (D + 1);
+}

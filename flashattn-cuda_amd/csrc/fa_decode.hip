@@ -1,0 +1,250 @@
+// fa_decode.hip — split-KV paged decode and its logsumexp combine for MI355X.
+//
+// No reference counterpart: the reference has no decode path. The math is
+// attention of one query token over the keys of its sequence, read through a
+// page table, computed per (sequence, head, split) as a normalised partial
+// (O_s, L_s), then merged by L = log sum_s exp(L_s), O = sum_s exp(L_s - L) O_s.
+//
+// Pool layout: [num_pages, H, 16, D] fp16, so the 16 tokens of one head in a
+// page are 16*D*2 contiguous bytes (4 KiB at D=128): one wave reads a page of
+// one head as fully coalesced 16-byte loads.
+//
+// Split kernel: one workgroup (4 waves) per (split, head, sequence). Wave w
+// walks pages p0+w, p0+w+4, ...; lane l covers token l/4 of the page and a
+// quarter of D. Each wave keeps its own running max/sum and fp32 partial
+// output; the four waves merge through LDS at the end.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "fa_mi355x.h"
+#include "fa_tile.hpp"
+
+namespace fa {
+
+constexpr int kPage = 16;
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = kDecThreads / 64;
+
+template <int D>
+__global__ void __launch_bounds__(kDecThreads)
+fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
+                       const f16* __restrict__ vpool, const int32_t* __restrict__ page_table,
+                       const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
+                       float* __restrict__ part_lse, int H, int max_pages, int num_pages,
+                       int S, float c) {
+  constexpr int DPL = D / 4;   // d per lane
+  constexpr int NV = DPL / 8;  // 16-byte vectors per lane per row
+  __shared__ float sh_o[kDecWaves][D];
+  __shared__ float sh_m[kDecWaves];
+  __shared__ float sh_l[kDecWaves];
+  __shared__ int sh_bad;
+
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tok = lane >> 2;   // token within the page
+  const int dq = lane & 3;     // quarter of D
+
+  if (tid == 0) sh_bad = 0;
+
+  int ctx = ctx_lens[b];
+  bool bad = false;
+  if (ctx < 0) { bad = true; ctx = 0; }
+  int pages = (ctx + kPage - 1) / kPage;
+  if (pages > max_pages) { bad = true; pages = max_pages; ctx = max_pages * kPage; }
+  const int chunk = (pages + S - 1) / S;
+  const int p0 = min(s * chunk, pages);
+  const int p1 = min(p0 + chunk, pages);
+
+  // Query slice of this lane as fp16 pairs.
+  const f16* qp = q + ((size_t)b * H + h) * D + dq * DPL;
+  f16x2 qv[DPL / 2];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    f16x8 x = *reinterpret_cast<const f16x8*>(qp + 8 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[4 * i + e] = f16x2{x[2 * e], x[2 * e + 1]};
+  }
+
+  float m = -INFINITY, l = 0.f;
+  float o[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+
+  const int32_t* pt = page_table + (size_t)b * max_pages;
+  for (int p = p0 + wave; p < p1; p += kDecWaves) {
+    const int pid = pt[p];
+    if (pid < 0 || pid >= num_pages) { bad = true; continue; }
+    const size_t base = ((size_t)pid * H + h) * (kPage * D) + (size_t)tok * D + dq * DPL;
+    f16x8 kv[NV], vv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const f16x8*>(vpool + base + 8 * i);
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dot = __builtin_amdgcn_fdot2(qv[4 * i + e], f16x2{kv[i][2 * e], kv[i][2 * e + 1]}, dot, false);
+      }
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    float st = dot * c;
+    if (p * kPage + tok >= ctx) st = -INFINITY;
+    float mp = st;
+    mp = fmaxf(mp, __shfl_xor(mp, 4, 64));
+    mp = fmaxf(mp, __shfl_xor(mp, 8, 64));
+    mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
+    mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+    const float m_new = fmaxf(m, mp);   // finite: token p*16 < ctx
+    const float alpha = (m_new == m) ? 1.f : exp2_hw(m - m_new);
+    const float pr = exp2_hw(st - m_new);
+    l = l * alpha + pr;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[8 * i + e] = fmaf(pr, (float)vv[i][e], o[8 * i + e] * alpha);
+    }
+    m = m_new;
+  }
+
+  // Sum the 16 token lanes that share a quarter of D.
+#pragma unroll
+  for (int sh = 4; sh < 64; sh <<= 1) {
+    l += __shfl_xor(l, sh, 64);
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] += __shfl_xor(o[i], sh, 64);
+  }
+  if (bad) sh_bad = 1;
+  if (tok == 0) {
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) sh_o[wave][dq * DPL + i] = o[i];
+    if (dq == 0) { sh_m[wave] = m; sh_l[wave] = l; }
+  }
+  __syncthreads();
+
+  const size_t pidx = ((size_t)b * H + h) * S + s;
+  if (tid < D) {
+    float M = sh_m[0];
+#pragma unroll
+    for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, sh_m[w]);
+    float acc = 0.f, z = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const float e = (sh_m[w] == -INFINITY) ? 0.f : exp2_hw(sh_m[w] - M);
+        acc += e * sh_o[w][tid];
+        z += e * sh_l[w];
+      }
+    }
+    float out = (z > 0.f) ? acc / z : 0.f;
+    float lse = (z > 0.f) ? (M + log2_hw(z)) * kLn2 : -INFINITY;
+    if (sh_bad) { out = NAN; lse = NAN; }
+    part_o[pidx * D + tid] = out;
+    if (tid == 0) part_lse[pidx] = lse;
+  }
+}
+
+// One workgroup of D threads per (b, h): thread d merges column d.
+template <int D>
+__global__ void __launch_bounds__(D)
+fa_lse_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse,
+                      f16* __restrict__ o, float* __restrict__ lse, int S) {
+  const int bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const float* ls = part_lse + (size_t)bh * S;
+  float M = -INFINITY;
+  bool nan = false;
+  for (int s = 0; s < S; ++s) {
+    const float x = ls[s];
+    nan |= (x != x);
+    M = fmaxf(M, x);
+  }
+  float out, L;
+  if (nan) {
+    out = NAN;
+    L = NAN;
+  } else if (M == -INFINITY) {
+    out = 0.f;
+    L = -INFINITY;
+  } else {
+    float z = 0.f;
+    for (int s = 0; s < S; ++s) z += exp2_hw((ls[s] - M) * kLog2e);
+    L = M + log2_hw(z) * kLn2;
+    float acc = 0.f;
+    const float* po = part_o + (size_t)bh * S * D + d;
+    for (int s = 0; s < S; ++s) {
+      const float w = exp2_hw((ls[s] - L) * kLog2e);
+      acc = fmaf(w, po[(size_t)s * D], acc);
+    }
+    out = acc;
+  }
+  o[(size_t)bh * D + d] = (f16)out;
+  if (lse != nullptr && d == 0) lse[bh] = L;
+}
+
+}  // namespace fa
+
+extern "C" int fa_decode_split_f16(const void* q, const void* k_pool, const void* v_pool,
+                                   const int32_t* page_table, const int32_t* ctx_lens,
+                                   int64_t B, int64_t H, int64_t D, int64_t page_size,
+                                   int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                                   float* part_o, float* part_lse, void* stream) {
+  using namespace fa;
+  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
+                              max_pages, num_pages, num_splits);
+  if (st != FA_OK) return st;
+  if (!part_o || !part_lse) return FA_ERR_NULL_POINTER;
+  const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)num_splits, (unsigned)H, (unsigned)B);
+  if (D == 128) {
+    hipLaunchKernelGGL((fa_decode_split_kernel<128>), grid, dim3(kDecThreads), 0, s,
+                       (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table,
+                       ctx_lens, part_o, part_lse, (int)H, (int)max_pages, (int)num_pages,
+                       (int)num_splits, c);
+  } else {
+    hipLaunchKernelGGL((fa_decode_split_kernel<64>), grid, dim3(kDecThreads), 0, s,
+                       (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table,
+                       ctx_lens, part_o, part_lse, (int)H, (int)max_pages, (int)num_pages,
+                       (int)num_splits, c);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FA_OK : -(int)e;
+}
+
+extern "C" int fa_lse_combine_f32(const float* part_o, const float* part_lse, int64_t B,
+                                  int64_t H, int64_t D, int64_t num_splits, void* o,
+                                  float* lse, void* stream) {
+  using namespace fa;
+  if (!part_o || !part_lse || !o) return FA_ERR_NULL_POINTER;
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
+  if (num_splits < 1 || num_splits > 16) return FA_ERR_NUM_SPLITS;
+  if (B * H > (int64_t(1) << 31) - 1) return FA_ERR_TOO_LARGE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (D == 128) {
+    hipLaunchKernelGGL((fa_lse_combine_kernel<128>), dim3((unsigned)(B * H)), dim3(128), 0, s,
+                       part_o, part_lse, (f16*)o, lse, (int)num_splits);
+  } else {
+    hipLaunchKernelGGL((fa_lse_combine_kernel<64>), dim3((unsigned)(B * H)), dim3(64), 0, s,
+                       part_o, part_lse, (f16*)o, lse, (int)num_splits);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FA_OK : -(int)e;
+}
+
+extern "C" int fa_decode_paged_f16(const void* q, const void* k_pool, const void* v_pool,
+                                   const int32_t* page_table, const int32_t* ctx_lens,
+                                   int64_t B, int64_t H, int64_t D, int64_t page_size,
+                                   int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                                   float* part_o, float* part_lse, void* o, float* lse,
+                                   void* stream) {
+  int st = fa_decode_split_f16(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
+                               max_pages, num_pages, num_splits, part_o, part_lse, stream);
+  if (st != FA_OK) return st;
+  return fa_lse_combine_f32(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
+}

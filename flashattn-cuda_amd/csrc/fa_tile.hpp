@@ -1,0 +1,141 @@
+// fa_tile.hpp — gfx950 building blocks shared by the forward kernel and the
+// layout probes: MFMA wrappers, LDS tile layouts, operand loaders, P packing.
+//
+// Matrix-core conventions (v_mfma_f32_32x32x16_f16, one wave64):
+//   A (32 x 16): lane l holds A[l % 32][8*(l/32) + i], i = 0..7
+//   B (16 x 32): lane l holds B[8*(l/32) + i][l % 32], i = 0..7
+//   C (32 x 32): lane l, register r holds C[8*(r/4) + 4*(l/32) + r%4][l % 32]
+// The layout probes in fa_probe.hip check these on the device.
+//
+// The forward kernel computes S^T = K Q^T (A = K tile from LDS, B = Q held in
+// registers), so lane l owns query l%32 and 16 of the 32 keys of a block; row
+// statistics are in-lane plus one exchange with lane l^32. It then computes
+// O^T = V^T P^T with P^T taken straight from the S^T accumulator (no LDS round
+// trip): the PV reduction index is the key, so keys may be visited in any
+// order as long as V^T and P^T agree. The order used is the S^T register order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 2^x on the hardware transcendental unit (v_exp_f32); 2^-inf = 0.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+// log2(x) on v_log_f32.
+__device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
+
+// Value of lane (l ^ 32).
+__device__ __forceinline__ float xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile layouts. A K or V tile is BC rows (keys) x D fp16, row stride 2*D
+// bytes, stored as 16-byte chunks (8 halves). Chunk c of row r lives at chunk
+// slot pos(r, c) of that row; pos is an XOR swizzle chosen so that the
+// operand reads below hit distinct LDS banks within each 16-lane group.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ int k_slot(int r, int c) {
+  if constexpr (D == 64) {
+    return c ^ ((r >> 1) & 7);
+  } else {
+    return c ^ (r & 15);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ int v_slot(int r, int c) {
+  if constexpr (D == 64) {
+    return c ^ (((r >> 1) & 1) << 2);
+  } else {
+    return c ^ ((r & 3) << 2);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ int k_off(int r, int c) { return r * (2 * D) + k_slot<D>(r, c) * 16; }
+
+template <int D>
+__device__ __forceinline__ int v_off(int r, int c) { return r * (2 * D) + v_slot<D>(r, c) * 16; }
+
+// A operand of S^T = K Q^T for key block kb (32 keys) and k-step kk (16 of D).
+template <int D>
+__device__ __forceinline__ f16x8 load_k_frag(const char* ks, int kb, int kk, int lane) {
+  const int r = 32 * kb + (lane & 31);
+  const int c = 2 * kk + (lane >> 5);
+  return *reinterpret_cast<const f16x8*>(ks + k_off<D>(r, c));
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane s supplies the
+// address of 4 consecutive halves M[s][0..3]; it receives
+// out[e] = M[4*e + s/4][s%4]. If lane s points at row (k0 + s/4),
+// columns (d0 + 4*(s%4)) .. +3 of a row-major [key][d] tile, lane s receives
+// the column d0 + s for keys k0 .. k0+3.
+__device__ __forceinline__ f16x4 lds_read_tr16(const char* p) {
+  typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+  fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)(p));
+  return __builtin_bit_cast(f16x4, v);
+}
+
+// A operand of O^T = V^T P^T for PV k-step j (16 keys of the 64-key tile) and
+// d-block db (32 of D). Slot i of lane l must hold V[key(j, i, l)][32*db + l%32]
+// with key(j, i, l) = 16*j + 8*(i/4) + 4*(l/32) + i%4, the key order of the
+// S^T accumulator registers (see pack_p).
+template <int D>
+__device__ __forceinline__ f16x8 load_v_frag(const char* vs, int j, int db, int lane) {
+  const int s = lane & 15;
+  const int hi = lane >> 5;
+  const int d = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  const int c = d >> 3;
+  const int half = (d >> 2) & 1;
+  const int r0 = 16 * j + 4 * hi + (s >> 2);
+  const int r1 = r0 + 8;
+  f16x4 lo = lds_read_tr16(vs + v_off<D>(r0, c) + 8 * half);
+  f16x4 up = lds_read_tr16(vs + v_off<D>(r1, c) + 8 * half);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+}
+
+// Key index (within a 64-key tile) held by register r of key block kb in lane l.
+__device__ __forceinline__ int st_key(int kb, int r, int lane) {
+  return 32 * kb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+
+// fp32 -> fp16 round-to-nearest-even, two at a time (v_cvt_pk_f16_f32).
+__device__ __forceinline__ f16x2 cvt2(float a, float b) {
+  return f16x2{(f16)a, (f16)b};
+}
+
+// B operand (P^T) of PV k-step j from the S^T accumulators p[2] of a tile.
+__device__ __forceinline__ f16x8 pack_p(const f32x16& p, int half_sel) {
+  const int b = 8 * half_sel;
+  f16x2 x0 = cvt2(p[b + 0], p[b + 1]);
+  f16x2 x1 = cvt2(p[b + 2], p[b + 3]);
+  f16x2 x2 = cvt2(p[b + 4], p[b + 5]);
+  f16x2 x3 = cvt2(p[b + 6], p[b + 7]);
+  return f16x8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+}
+
+}  // namespace fa

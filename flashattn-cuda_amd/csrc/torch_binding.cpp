@@ -1,0 +1,244 @@
+// torch_binding.cpp — the reference's torch-extension surface, over the C ABI.
+//
+// Mirrors the reference module built from cuda/flash_attn_fa3_db_full.cu:
+//   forward(Q, K, V)      -> [O half [B,H,N,D], L float [B,H,N]]   (:405-408)
+//   forward_only(Q, K, V) -> O                                      (:410-413)
+// with the same argument checks and messages as fa3db_full_forward_impl
+// (:352-363), the same fp16 cast of the inputs (:366-368), fresh outputs on
+// Q's device (:370-376) and an asynchronous launch on the current stream
+// (:378-399). Additions: a `causal` flag (default false) and D = 128, plus the
+// paged decode entry points. Kernels are reached only through the C ABI in
+// include/fa_mi355x.h; this file makes no HIP call of its own.
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <vector>
+
+#include "fa_mi355x.h"
+#include "fa_probe.h"
+
+namespace {
+
+void* current_stream(const torch::Tensor& t) {
+  return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+void check_status(int st, const char* what) {
+  TORCH_CHECK(st == FA_OK, what, " failed: ", fa_status_str(st), " (status ", st, ")");
+}
+
+std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Tensor K,
+                                                     torch::Tensor V, bool want_L, bool causal) {
+  TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Q/K/V must be CUDA tensors");
+  TORCH_CHECK(Q.dim() == 4, "Q must be 4D [B, H, N, D]");
+  const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
+  TORCH_CHECK(D == 64 || D == 128, "Head dimension must be 64 or 128");
+  TORCH_CHECK(N > 0, "N must be > 0");
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(),
+              "K and V must have the same shape as Q (self-attention only)");
+  TORCH_CHECK(K.device() == Q.device() && V.device() == Q.device(),
+              "Q/K/V must be on the same device");
+  TORCH_CHECK(Q.is_floating_point() && K.is_floating_point() && V.is_floating_point(),
+              "Q/K/V must be floating point");
+
+  const c10::DeviceGuard guard(Q.device());
+  const int64_t BH = B * H;
+  auto Qh = Q.to(torch::kHalf).reshape({BH, N, D}).contiguous();
+  auto Kh = K.to(torch::kHalf).reshape({BH, N, D}).contiguous();
+  auto Vh = V.to(torch::kHalf).reshape({BH, N, D}).contiguous();
+  auto O = torch::empty({BH, N, D}, Qh.options());
+  torch::Tensor L;
+  float* L_ptr = nullptr;
+  if (want_L) {
+    L = torch::empty({BH, N}, Qh.options().dtype(torch::kFloat));
+    L_ptr = L.data_ptr<float>();
+  }
+  const int st = fa_fwd_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H,
+                            N, D, causal ? 1 : 0, current_stream(Qh));
+  check_status(st, "fa_fwd_f16");
+  return {O.reshape({B, H, N, D}), want_L ? L.reshape({B, H, N}) : torch::Tensor()};
+}
+
+std::vector<torch::Tensor> forward(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal) {
+  auto r = forward_impl(Q, K, V, /*want_L=*/true, causal);
+  return {r.first, r.second};
+}
+
+torch::Tensor forward_only(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal) {
+  return forward_impl(Q, K, V, /*want_L=*/false, causal).first;
+}
+
+struct DecodeArgs {
+  int64_t B, H, D, page_size, max_pages, num_pages;
+};
+
+DecodeArgs check_decode(const torch::Tensor& q, const torch::Tensor& k_pool,
+                        const torch::Tensor& v_pool, const torch::Tensor& page_table,
+                        const torch::Tensor& ctx_lens) {
+  TORCH_CHECK(q.is_cuda() && k_pool.is_cuda() && v_pool.is_cuda() && page_table.is_cuda() &&
+                  ctx_lens.is_cuda(),
+              "q/k_pool/v_pool/page_table/ctx_lens must be CUDA tensors");
+  TORCH_CHECK(q.dim() == 3, "q must be 3D [B, H, D]");
+  TORCH_CHECK(k_pool.dim() == 4, "k_pool must be 4D [num_pages, H, page_size, D]");
+  TORCH_CHECK(v_pool.sizes() == k_pool.sizes(), "v_pool must have the same shape as k_pool");
+  TORCH_CHECK(q.scalar_type() == torch::kHalf && k_pool.scalar_type() == torch::kHalf &&
+                  v_pool.scalar_type() == torch::kHalf,
+              "q/k_pool/v_pool must be float16");
+  TORCH_CHECK(page_table.dim() == 2 && page_table.scalar_type() == torch::kInt,
+              "page_table must be int32 [B, max_pages]");
+  TORCH_CHECK(ctx_lens.dim() == 1 && ctx_lens.scalar_type() == torch::kInt,
+              "ctx_lens must be int32 [B]");
+  TORCH_CHECK(q.is_contiguous() && k_pool.is_contiguous() && v_pool.is_contiguous() &&
+                  page_table.is_contiguous() && ctx_lens.is_contiguous(),
+              "decode tensors must be contiguous");
+  DecodeArgs a;
+  a.B = q.size(0);
+  a.H = q.size(1);
+  a.D = q.size(2);
+  a.num_pages = k_pool.size(0);
+  a.page_size = k_pool.size(2);
+  a.max_pages = page_table.size(1);
+  TORCH_CHECK(k_pool.size(1) == a.H && k_pool.size(3) == a.D,
+              "k_pool must be [num_pages, H, page_size, D] with q's H and D");
+  TORCH_CHECK(page_table.size(0) == a.B && ctx_lens.size(0) == a.B,
+              "page_table and ctx_lens must have q's batch size");
+  auto dev = q.device();
+  TORCH_CHECK(k_pool.device() == dev && v_pool.device() == dev && page_table.device() == dev &&
+                  ctx_lens.device() == dev,
+              "decode tensors must be on the same device");
+  return a;
+}
+
+std::vector<torch::Tensor> decode_partials(torch::Tensor q, torch::Tensor k_pool,
+                                           torch::Tensor v_pool, torch::Tensor page_table,
+                                           torch::Tensor ctx_lens, int64_t num_splits) {
+  const DecodeArgs a = check_decode(q, k_pool, v_pool, page_table, ctx_lens);
+  const c10::DeviceGuard guard(q.device());
+  auto part_o = torch::empty({a.B, a.H, num_splits, a.D}, q.options().dtype(torch::kFloat));
+  auto part_lse = torch::empty({a.B, a.H, num_splits}, q.options().dtype(torch::kFloat));
+  const int st = fa_decode_split_f16(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                                     page_table.data_ptr<int32_t>(), ctx_lens.data_ptr<int32_t>(),
+                                     a.B, a.H, a.D, a.page_size, a.max_pages, a.num_pages,
+                                     num_splits, part_o.data_ptr<float>(),
+                                     part_lse.data_ptr<float>(), current_stream(q));
+  check_status(st, "fa_decode_split_f16");
+  return {part_o, part_lse};
+}
+
+std::vector<torch::Tensor> lse_combine(torch::Tensor part_o, torch::Tensor part_lse) {
+  TORCH_CHECK(part_o.is_cuda() && part_lse.is_cuda(), "part_o/part_lse must be CUDA tensors");
+  TORCH_CHECK(part_o.dim() == 4 && part_o.scalar_type() == torch::kFloat && part_o.is_contiguous(),
+              "part_o must be contiguous float32 [B, H, num_splits, D]");
+  TORCH_CHECK(part_lse.dim() == 3 && part_lse.scalar_type() == torch::kFloat &&
+                  part_lse.is_contiguous(),
+              "part_lse must be contiguous float32 [B, H, num_splits]");
+  const int64_t B = part_o.size(0), H = part_o.size(1), S = part_o.size(2), D = part_o.size(3);
+  TORCH_CHECK(part_lse.size(0) == B && part_lse.size(1) == H && part_lse.size(2) == S,
+              "part_lse must be [B, H, num_splits] matching part_o");
+  const c10::DeviceGuard guard(part_o.device());
+  auto o = torch::empty({B, H, D}, part_o.options().dtype(torch::kHalf));
+  auto lse = torch::empty({B, H}, part_o.options());
+  const int st = fa_lse_combine_f32(part_o.data_ptr<float>(), part_lse.data_ptr<float>(), B, H, D,
+                                    S, o.data_ptr(), lse.data_ptr<float>(), current_stream(part_o));
+  check_status(st, "fa_lse_combine_f32");
+  return {o, lse};
+}
+
+std::vector<torch::Tensor> decode_paged(torch::Tensor q, torch::Tensor k_pool, torch::Tensor v_pool,
+                                        torch::Tensor page_table, torch::Tensor ctx_lens,
+                                        int64_t num_splits) {
+  const DecodeArgs a = check_decode(q, k_pool, v_pool, page_table, ctx_lens);
+  const c10::DeviceGuard guard(q.device());
+  auto ws = torch::empty({fa_decode_workspace_floats(a.B, a.H, a.D, num_splits)},
+                         q.options().dtype(torch::kFloat));
+  float* part_o = ws.data_ptr<float>();
+  float* part_lse = part_o + a.B * a.H * num_splits * a.D;
+  auto o = torch::empty({a.B, a.H, a.D}, q.options());
+  auto lse = torch::empty({a.B, a.H}, q.options().dtype(torch::kFloat));
+  const int st = fa_decode_paged_f16(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                                     page_table.data_ptr<int32_t>(), ctx_lens.data_ptr<int32_t>(),
+                                     a.B, a.H, a.D, a.page_size, a.max_pages, a.num_pages,
+                                     num_splits, part_o, part_lse, o.data_ptr(),
+                                     lse.data_ptr<float>(), current_stream(q));
+  check_status(st, "fa_decode_paged_f16");
+  return {o, lse};
+}
+
+// ---- layout probes (test support) ----
+torch::Tensor probe_mfma32(torch::Tensor a, torch::Tensor b, int64_t variant) {
+  TORCH_CHECK(a.is_cuda() && a.sizes() == torch::IntArrayRef({32, 16}) && a.scalar_type() == torch::kHalf);
+  TORCH_CHECK(b.is_cuda() && b.sizes() == torch::IntArrayRef({16, 32}) && b.scalar_type() == torch::kHalf);
+  auto ac = a.contiguous(), bc = b.contiguous();
+  auto c = torch::empty({32, 32}, a.options().dtype(torch::kFloat));
+  check_status(fa_probe_mfma32(ac.data_ptr(), bc.data_ptr(), c.data_ptr<float>(), (int)variant,
+                               current_stream(a)), "fa_probe_mfma32");
+  return c;
+}
+
+torch::Tensor probe_mfma16(torch::Tensor a, torch::Tensor b, int64_t variant) {
+  TORCH_CHECK(a.is_cuda() && a.sizes() == torch::IntArrayRef({16, 32}) && a.scalar_type() == torch::kHalf);
+  TORCH_CHECK(b.is_cuda() && b.sizes() == torch::IntArrayRef({32, 16}) && b.scalar_type() == torch::kHalf);
+  auto ac = a.contiguous(), bc = b.contiguous();
+  auto c = torch::empty({16, 16}, a.options().dtype(torch::kFloat));
+  check_status(fa_probe_mfma16(ac.data_ptr(), bc.data_ptr(), c.data_ptr<float>(), (int)variant,
+                               current_stream(a)), "fa_probe_mfma16");
+  return c;
+}
+
+torch::Tensor probe_tr16_raw(torch::Tensor in) {
+  TORCH_CHECK(in.is_cuda() && in.numel() == 256 && in.element_size() == 2);
+  auto ic = in.contiguous();
+  auto out = torch::empty({64, 4}, in.options());
+  check_status(fa_probe_tr16_raw(ic.data_ptr(), out.data_ptr(), current_stream(in)),
+               "fa_probe_tr16_raw");
+  return out;
+}
+
+std::vector<torch::Tensor> probe_frags(torch::Tensor tile) {
+  TORCH_CHECK(tile.is_cuda() && tile.dim() == 2 && tile.size(0) == 64 &&
+              (tile.size(1) == 64 || tile.size(1) == 128) && tile.scalar_type() == torch::kHalf);
+  const int64_t D = tile.size(1);
+  auto tc = tile.contiguous();
+  auto kout = torch::empty({2, D / 16, 64, 8}, tile.options());
+  auto vout = torch::empty({4, D / 32, 64, 8}, tile.options());
+  check_status(fa_probe_frags(tc.data_ptr(), kout.data_ptr(), vout.data_ptr(), D, current_stream(tile)),
+               "fa_probe_frags");
+  return {kout, vout};
+}
+
+torch::Tensor probe_chain(torch::Tensor q, torch::Tensor k, torch::Tensor v) {
+  TORCH_CHECK(q.is_cuda() && q.dim() == 2 && q.size(0) == 32 && q.scalar_type() == torch::kHalf);
+  const int64_t D = q.size(1);
+  TORCH_CHECK(D == 64 || D == 128);
+  TORCH_CHECK(k.sizes() == torch::IntArrayRef({64, D}) && v.sizes() == torch::IntArrayRef({64, D}));
+  auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
+  auto o = torch::empty({32, D}, q.options().dtype(torch::kFloat));
+  check_status(fa_probe_chain(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr<float>(), D,
+                              current_stream(q)), "fa_probe_chain");
+  return o;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("forward", &forward, "FlashAttention forward: returns [O half, L float]",
+        py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
+  m.def("forward_only", &forward_only, "FlashAttention forward, O only",
+        py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
+  m.def("decode_paged", &decode_paged, "split-KV paged decode: returns [O half, L float]",
+        py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("page_table"),
+        py::arg("ctx_lens"), py::arg("num_splits") = 16);
+  m.def("decode_partials", &decode_partials, "split pass only: returns [part_o, part_lse]",
+        py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("page_table"),
+        py::arg("ctx_lens"), py::arg("num_splits") = 16);
+  m.def("lse_combine", &lse_combine, "combine pass: returns [O half, L float]",
+        py::arg("part_o"), py::arg("part_lse"));
+  m.def("probe_mfma32", &probe_mfma32);
+  m.def("probe_mfma16", &probe_mfma16);
+  m.def("probe_tr16_raw", &probe_tr16_raw);
+  m.def("probe_frags", &probe_frags);
+  m.def("probe_chain", &probe_chain);
+  m.def("abi_version", &fa_abi_version);
+}

@@ -1,0 +1,126 @@
+/*
+ * fa_mi355x.h — C ABI of the MI355X (gfx950) FlashAttention forward and the
+ * split-KV paged decode.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * passed as void*. The library never allocates, never synchronises the host
+ * and keeps no mutable global state: it is re-entrant and stream-ordered.
+ * Buffers (including the decode split workspace) belong to the caller.
+ *
+ * Status codes: 0 = ok, > 0 = invalid argument (fa_status_str names it),
+ * < 0 = a HIP error, negated (-(int)hipError_t).
+ *
+ * Tensor layouts (all contiguous, row-major):
+ *   q, k, v, o : fp16 [B, H, N, D]        (bh = b*H + h; row stride D)
+ *   lse        : fp32 [B, H, N]           natural-log logsumexp of the scaled
+ *                                         logits S = q k^T / sqrt(D)
+ *   k_pool,    : fp16 [num_pages, H, page_size, D]   head-major pages
+ *   v_pool
+ *   page_table : int32 [B, max_pages]     page ids of each sequence, in order
+ *   ctx_lens   : int32 [B]                tokens per sequence
+ *   part_o     : fp32 [B, H, num_splits, D]   normalised split partials
+ *   part_lse   : fp32 [B, H, num_splits]      split logsumexp (-inf if empty)
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+enum fa_status_code {
+  FA_OK = 0,
+  FA_ERR_NULL_POINTER = 1,   /* a required pointer is NULL */
+  FA_ERR_HEAD_DIM = 2,       /* D is not 64 or 128 */
+  FA_ERR_SEQ_LEN = 3,        /* N <= 0 */
+  FA_ERR_BATCH_HEADS = 4,    /* B <= 0 or H <= 0 */
+  FA_ERR_ALIGNMENT = 5,      /* a tensor pointer is not 16-byte aligned */
+  FA_ERR_TOO_LARGE = 6,      /* a size exceeds the kernels' index range */
+  FA_ERR_PAGE_SIZE = 7,      /* page_size is not 16 */
+  FA_ERR_NUM_SPLITS = 8,     /* num_splits outside [1, 16] */
+  FA_ERR_MAX_PAGES = 9,      /* max_pages <= 0 */
+  FA_ERR_NUM_PAGES = 10      /* num_pages <= 0 */
+};
+
+/* Human-readable name of a status code (static storage). */
+const char* fa_status_str(int status);
+
+/* FA_ABI_VERSION of the built library. */
+int fa_abi_version(void);
+
+/*
+ * Host-only argument check of fa_fwd_f16 (no HIP call; runs without a GPU).
+ * Replaces the argument checks of the reference launcher
+ * fa3db_full_forward_impl (cuda/flash_attn_fa3_db_full.cu:352-363), widened to
+ * D in {64, 128}.
+ */
+int fa_validate_fwd(const void* q, const void* k, const void* v, const void* o,
+                    int64_t B, int64_t H, int64_t N, int64_t D);
+
+/*
+ * Attention forward: o = softmax(q k^T / sqrt(D) [+ causal mask]) v, and, if
+ * lse != NULL, the per-row logsumexp. lse == NULL is the O-only variant; its o
+ * is bitwise equal to the o written with lse != NULL.
+ * causal != 0: query i sees keys j <= i.
+ * Replaces fa3db_full_forward_impl (cuda/flash_attn_fa3_db_full.cu:349-403):
+ * want_L=true <-> lse != NULL (:405-408), want_L=false <-> lse == NULL
+ * (:410-413). The causal flag and D=128 have no reference counterpart.
+ */
+int fa_fwd_f16(const void* q, const void* k, const void* v, void* o, float* lse,
+               int64_t B, int64_t H, int64_t N, int64_t D, int causal,
+               void* stream);
+
+/*
+ * Host-only argument check of the decode entry points. No reference
+ * counterpart (the reference has no decode path).
+ */
+int fa_validate_decode(const void* q, const void* k_pool, const void* v_pool,
+                       const int32_t* page_table, const int32_t* ctx_lens,
+                       int64_t B, int64_t H, int64_t D, int64_t page_size,
+                       int64_t max_pages, int64_t num_pages, int64_t num_splits);
+
+/* Floats of split workspace the caller provides: part_o then part_lse. */
+int64_t fa_decode_workspace_floats(int64_t B, int64_t H, int64_t D,
+                                   int64_t num_splits);
+
+/*
+ * Split pass of the paged decode: for each (sequence b, head h, split s) the
+ * normalised partial attention of q[b,h] over the split's pages.
+ * Sequence b has ceil(ctx_lens[b]/page_size) pages, divided into num_splits
+ * runs of ceil(pages/num_splits) pages. An empty split writes part_o = 0 and
+ * part_lse = -inf. A page id outside [0, num_pages) or ctx_lens[b] beyond
+ * max_pages*page_size makes every partial of that sequence NaN (no memory
+ * outside the pool is read). No reference counterpart.
+ */
+int fa_decode_split_f16(const void* q, const void* k_pool, const void* v_pool,
+                        const int32_t* page_table, const int32_t* ctx_lens,
+                        int64_t B, int64_t H, int64_t D, int64_t page_size,
+                        int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                        float* part_o, float* part_lse, void* stream);
+
+/*
+ * Combine pass: L = log sum_s exp(part_lse_s); o = sum_s exp(part_lse_s - L)
+ * part_o_s, written as fp16 o [B, H, D] and fp32 lse [B, H] (lse may be NULL).
+ * If every split is empty, o = 0 and lse = -inf. No reference counterpart.
+ */
+int fa_lse_combine_f32(const float* part_o, const float* part_lse,
+                       int64_t B, int64_t H, int64_t D, int64_t num_splits,
+                       void* o, float* lse, void* stream);
+
+/* Split pass then combine pass, both on `stream`. No reference counterpart. */
+int fa_decode_paged_f16(const void* q, const void* k_pool, const void* v_pool,
+                        const int32_t* page_table, const int32_t* ctx_lens,
+                        int64_t B, int64_t H, int64_t D, int64_t page_size,
+                        int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                        float* part_o, float* part_lse, void* o, float* lse,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */

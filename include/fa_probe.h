@@ -1,0 +1,45 @@
+/*
+ * fa_probe.h — device probes of the gfx950 matrix-core and LDS layouts that
+ * the forward kernel relies on. Test support only; the analogue of the
+ * reference's mma probe module (cuda/mma_probe.cu:256-320, exported to Python
+ * at cuda/mma_probe.cu:314-320), rebuilt for v_mfma_f32_32x32x16_f16,
+ * v_mfma_f32_16x16x32_f16 and ds_read_b64_tr_b16.
+ *
+ * All buffers are device pointers; every probe runs one wave on `stream`.
+ * Return: 0 ok, > 0 bad argument, < 0 negated hipError_t.
+ */
+#ifndef FA_PROBE_H
+#define FA_PROBE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* c[32][32] = a[32][16] @ b[16][32] (fp16 in, fp32 out) with the lane layout
+ * the kernels assume; variant 1 swaps A's k-halves (negative control). */
+int fa_probe_mfma32(const void* a, const void* b, float* c, int variant, void* stream);
+
+/* c[16][16] = a[16][32] @ b[32][16]; variant 1 reverses A's k-groups. */
+int fa_probe_mfma16(const void* a, const void* b, float* c, int variant, void* stream);
+
+/* LDS holds the 256 halves of `in`; lane l executes ds_read_b64_tr_b16 at byte
+ * offset 8*l and writes its 4 halves to out[4*l .. 4*l+3]. */
+int fa_probe_tr16_raw(const void* in, void* out, void* stream);
+
+/* Stores a [64][D] fp16 tile with the forward kernel's K and V LDS layouts and
+ * dumps every operand fragment the kernel reads:
+ *   kout [2][D/16][64][8], vout [4][D/32][64][8] fp16. D in {64, 128}. */
+int fa_probe_frags(const void* tile, void* kout, void* vout, int64_t D, void* stream);
+
+/* One 64-key tile through the kernel's loaders and MFMA chain without softmax:
+ * o[32][D] = fp16(q[32][D] @ k[64][D]^T) @ v[64][D], fp32 out. */
+int fa_probe_chain(const void* q, const void* k, const void* v, float* o, int64_t D,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_PROBE_H */

@@ -1,0 +1,295 @@
+"""CPU restatement of the reference's naive attention: TEST INFRASTRUCTURE ONLY.
+
+This module is the checker for the HIP path. Only tests/, the smoke() check in
+__graft_entry__.py and the cpu_baseline leg of bench.py may import it. The
+product path (the HIP library and its torch binding) never calls it and has no
+CPU fallback.
+
+What it restates
+----------------
+* ``naive_attention`` follows ref/naive_attn.py:23-38:
+    scale = D**-0.5                      (ref/naive_attn.py:24)
+    S = (Q @ K^T) * scale                (ref/naive_attn.py:27)
+    P = softmax(S, -1)                   (ref/naive_attn.py:30)
+    O = P @ V                            (ref/naive_attn.py:33)
+    L = logsumexp(S, -1)                 (ref/naive_attn.py:36)
+  The reference's tests feed it half-cast inputs in fp32 math
+  (tests/test_fa3_db_full.py:34-35); ``half_cast`` does that cast.
+  The ``causal`` flag is new (the reference has no causal path,
+  README.md:321-325): key j is visible to query i iff j <= i.
+* ``gather_pages``, ``decode_attention``, ``split_partials`` and
+  ``lse_combine`` are the paged split-KV decode and its logsumexp merge. The
+  reference has no decode path; these restate flash-decoding from its
+  definition: attention of one query over the gathered keys, split into
+  chunks, merged with L = log sum_s exp(L_s), O = sum_s exp(L_s - L) O_s.
+* ``attention_bruteforce`` is a pure-Python double loop in float64 for tiny
+  inputs; tests use it to pin the numpy path.
+
+Pinning status (each function is checked in tests/test_oracle.py):
+* naive_attention: brute force on tiny inputs, closed forms (N=1, Q=0,
+  equal keys, constant V, causal row 0, causal last row == non-causal),
+  row-permutation invariance, committed golden fixtures.
+* decode_attention / gather_pages: equals naive_attention of the single query
+  over the contiguous keys; gather equals a direct index walk.
+* split_partials + lse_combine: combine of any split count equals the
+  unsplit result; one split is the identity; empty splits carry weight 0.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+LN2 = math.log(2.0)
+
+
+def half_cast(x: np.ndarray) -> np.ndarray:
+    """fp16 round-trip then float32, the cast of tests/test_fa3_db_full.py:34."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def _softmax_lse(S: np.ndarray):
+    """Row softmax and natural-log logsumexp of S (last axis), stable form.
+
+    Rows that are entirely -inf give P = 0 and L = -inf.
+    """
+    m = S.max(axis=-1, keepdims=True)
+    m_safe = np.where(np.isfinite(m), m, 0.0).astype(S.dtype)
+    E = np.exp(S - m_safe)
+    l = E.sum(axis=-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        P = np.where(l > 0, E / np.where(l > 0, l, 1), 0.0).astype(S.dtype)
+        L = (m_safe + np.log(l))[..., 0]
+    L = np.where(l[..., 0] > 0, L, -np.inf).astype(S.dtype)
+    return P, L
+
+
+def naive_attention(Q, K, V, causal: bool = False, dtype=np.float32):
+    """O, L = naive attention over [B, H, N, D] arrays (ref/naive_attn.py:10-38).
+
+    Math runs in ``dtype`` (float32 by default, like the reference's fp32 torch
+    path on half-cast inputs). Loops over (b, h) so one N x N score matrix is
+    alive at a time.
+    """
+    Q = np.asarray(Q, dtype=dtype)
+    K = np.asarray(K, dtype=dtype)
+    V = np.asarray(V, dtype=dtype)
+    B, H, N, D = Q.shape
+    Nk = K.shape[2]
+    scale = dtype(D ** -0.5) if dtype is not np.float64 else D ** -0.5
+    O = np.empty((B, H, N, V.shape[3]), dtype=dtype)
+    L = np.empty((B, H, N), dtype=dtype)
+    mask = None
+    if causal:
+        mask = np.arange(Nk)[None, :] > np.arange(N)[:, None]
+    for b in range(B):
+        for h in range(H):
+            S = (Q[b, h] @ K[b, h].T) * scale
+            if mask is not None:
+                S = np.where(mask, -np.inf, S).astype(dtype)
+            P, l = _softmax_lse(S)
+            O[b, h] = P @ V[b, h]
+            L[b, h] = l
+    return O, L
+
+
+def attention_bruteforce(q, k, v, causal: bool = False):
+    """Pure-Python float64 attention for one head: q [N][D], k/v [Nk][D].
+
+    Written as explicit loops over the definition so it shares no code with
+    ``naive_attention``. Use only for N, D of a few dozen.
+    """
+    n, d = len(q), len(q[0])
+    nk = len(k)
+    scale = 1.0 / math.sqrt(d)
+    O, L = [], []
+    for i in range(n):
+        s = []
+        for j in range(nk):
+            if causal and j > i:
+                continue
+            acc = 0.0
+            for t in range(d):
+                acc += float(q[i][t]) * float(k[j][t])
+            s.append((j, acc * scale))
+        m = max(x for _, x in s)
+        z = sum(math.exp(x - m) for _, x in s)
+        o = [0.0] * len(v[0])
+        for j, x in s:
+            w = math.exp(x - m) / z
+            for t in range(len(v[0])):
+                o[t] += w * float(v[j][t])
+        O.append(o)
+        L.append(m + math.log(z))
+    return O, L
+
+
+# ----------------------------------------------------------------------------
+# Paged split-KV decode
+# ----------------------------------------------------------------------------
+# Pool layout (the build's choice, documented in include/fa_mi355x.h):
+#   k_pool, v_pool : [num_pages, H, page_size, D]  (head-major pages)
+#   page_table     : [B, max_pages] int32, entry p of sequence b holds tokens
+#                    [p*page_size, (p+1)*page_size) of that sequence
+#   ctx_lens       : [B] int32, tokens in sequence b
+# ----------------------------------------------------------------------------
+
+def gather_pages(pool, page_table, ctx_len: int, b: int, h: int):
+    """Contiguous [ctx_len, D] rows of head h of sequence b, read through the page table."""
+    page_size = pool.shape[2]
+    n_pages = (ctx_len + page_size - 1) // page_size
+    ids = np.asarray(page_table[b, :n_pages], dtype=np.int64)
+    rows = pool[ids, h]                          # [n_pages, page_size, D]
+    return rows.reshape(n_pages * page_size, pool.shape[3])[:ctx_len]
+
+
+def decode_attention(q, k_pool, v_pool, page_table, ctx_lens, dtype=np.float32):
+    """O [B, H, D], L [B, H] of one query token per sequence over its paged keys.
+
+    Equals ``naive_attention`` of the single query against the gathered
+    contiguous K/V of each (b, h).
+    """
+    q = np.asarray(q, dtype=dtype)
+    B, H, D = q.shape
+    O = np.zeros((B, H, v_pool.shape[3]), dtype=dtype)
+    L = np.full((B, H), -np.inf, dtype=dtype)
+    scale = dtype(D ** -0.5) if dtype is not np.float64 else D ** -0.5
+    for b in range(B):
+        n = int(ctx_lens[b])
+        if n <= 0:
+            continue
+        for h in range(H):
+            k = gather_pages(k_pool, page_table, n, b, h).astype(dtype)
+            v = gather_pages(v_pool, page_table, n, b, h).astype(dtype)
+            s = (k @ q[b, h]) * scale
+            p, l = _softmax_lse(s[None, :])
+            O[b, h] = p[0] @ v
+            L[b, h] = l[0]
+    return O, L
+
+
+def split_bounds(ctx_len: int, page_size: int, num_splits: int):
+    """Page ranges [p0, p1) of each split: ceil(pages / num_splits) pages per split."""
+    n_pages = (ctx_len + page_size - 1) // page_size
+    chunk = (n_pages + num_splits - 1) // num_splits if n_pages > 0 else 0
+    out = []
+    for s in range(num_splits):
+        p0 = min(s * chunk, n_pages)
+        p1 = min(p0 + chunk, n_pages)
+        out.append((p0, p1))
+    return out
+
+
+def split_partials(q, k_pool, v_pool, page_table, ctx_lens, num_splits: int,
+                   dtype=np.float32):
+    """Per-split normalised partials O_s [B, H, S, D] and L_s [B, H, S].
+
+    An empty split has O_s = 0 and L_s = -inf.
+    """
+    q = np.asarray(q, dtype=dtype)
+    B, H, D = q.shape
+    page_size = k_pool.shape[2]
+    Dv = v_pool.shape[3]
+    Os = np.zeros((B, H, num_splits, Dv), dtype=dtype)
+    Ls = np.full((B, H, num_splits), -np.inf, dtype=dtype)
+    scale = dtype(D ** -0.5) if dtype is not np.float64 else D ** -0.5
+    for b in range(B):
+        n = int(ctx_lens[b])
+        for h in range(H):
+            k = gather_pages(k_pool, page_table, n, b, h).astype(dtype)
+            v = gather_pages(v_pool, page_table, n, b, h).astype(dtype)
+            for s, (p0, p1) in enumerate(split_bounds(n, page_size, num_splits)):
+                t0, t1 = p0 * page_size, min(p1 * page_size, n)
+                if t1 <= t0:
+                    continue
+                sc = (k[t0:t1] @ q[b, h]) * scale
+                p, l = _softmax_lse(sc[None, :])
+                Os[b, h, s] = p[0] @ v[t0:t1]
+                Ls[b, h, s] = l[0]
+    return Os, Ls
+
+
+def lse_combine(Os, Ls):
+    """Merge normalised split partials: L = log sum_s exp(L_s); O = sum_s exp(L_s - L) O_s.
+
+    Splits with L_s = -inf have weight 0. If every split is empty, O = 0 and
+    L = -inf.
+    """
+    Os = np.asarray(Os)
+    Ls = np.asarray(Ls)
+    M = Ls.max(axis=-1, keepdims=True)
+    M_safe = np.where(np.isfinite(M), M, 0.0)
+    w = np.exp(Ls - M_safe)
+    z = w.sum(axis=-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        L = np.where(z[..., 0] > 0, (M_safe + np.log(z))[..., 0], -np.inf)
+        wn = np.where(z > 0, w / np.where(z > 0, z, 1), 0.0)
+    O = (wn[..., None] * Os).sum(axis=-2)
+    return O.astype(Os.dtype), L.astype(Ls.dtype)
+
+
+# ----------------------------------------------------------------------------
+# Seeded synthetic inputs (the BASELINE configs)
+# ----------------------------------------------------------------------------
+
+def randn_f16(rng: np.random.Generator, shape, amp: float = 1.0) -> np.ndarray:
+    """N(0, amp^2) samples rounded to fp16 (the GPU sees exactly these bits)."""
+    x = rng.standard_normal(size=shape, dtype=np.float32)
+    if amp != 1.0:
+        x *= np.float32(amp)
+    return x.astype(np.float16)
+
+
+def make_fwd_inputs(B, H, N, D, seed=42, amp=1.0):
+    """Q, K, V fp16 [B, H, N, D] ~ N(0, amp^2) from ``seed``."""
+    rng = np.random.default_rng(seed)
+    return (randn_f16(rng, (B, H, N, D), amp), randn_f16(rng, (B, H, N, D), amp),
+            randn_f16(rng, (B, H, N, D), amp))
+
+
+def ragged_n(seed: int, lo: int = 1000, hi: int = 5000, tiles=(32, 64, 128)) -> int:
+    """N ~ U[lo, hi] from ``seed``, redrawn until it is a multiple of no tile size."""
+    rng = np.random.default_rng(seed)
+    while True:
+        n = int(rng.integers(lo, hi + 1))
+        if all(n % t for t in tiles):
+            return n
+
+
+def make_ragged_inputs(B=2, H=8, D=64, seed=7, hot_frac=0.05):
+    """Config 4: ragged N, Q/K ~ N(0,1) with a seeded subset of rows at std 3.
+
+    A row of Q (or K) chosen with probability ``hot_frac`` is redrawn with
+    std 3, so logits on those rows have std ~9 and exercise the rescale.
+    """
+    N = ragged_n(seed)
+    rng = np.random.default_rng(seed + 1)
+    Q = rng.standard_normal((B, H, N, D), dtype=np.float32)
+    K = rng.standard_normal((B, H, N, D), dtype=np.float32)
+    V = rng.standard_normal((B, H, N, D), dtype=np.float32)
+    hq = rng.random((B, H, N)) < hot_frac
+    hk = rng.random((B, H, N)) < hot_frac
+    Q[hq] *= 3.0
+    K[hk] *= 3.0
+    return N, Q.astype(np.float16), K.astype(np.float16), V.astype(np.float16)
+
+
+def make_decode_meta(B=32, ctx_lo=512, ctx_hi=32768, page_size=16, seed=5):
+    """Context lengths and a random page-table permutation for the decode config.
+
+    Returns (ctx_lens int32 [B], page_table int32 [B, max_pages], num_pages).
+    Every page of the pool is used exactly once; the page ids of all sequences
+    together are a random permutation of range(num_pages).
+    """
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(ctx_lo, ctx_hi + 1, size=B).astype(np.int32)
+    pages = (ctx + page_size - 1) // page_size
+    num_pages = int(pages.sum())
+    max_pages = int(pages.max())
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = np.zeros((B, max_pages), dtype=np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    return ctx, table, num_pages

@@ -1,0 +1,113 @@
+"""CPU tier: the C-ABI library loads, exports every declared symbol, and rejects
+bad arguments before any HIP call (the reference's argument checks,
+cuda/flash_attn_fa3_db_full.cu:352-363, restated as status codes)."""
+import ctypes as C
+
+import pytest
+
+
+def test_library_exports_every_header_symbol(capi):
+    lib = capi.load()
+    names = capi.header_symbols()
+    assert "fa_fwd_f16" in names and "fa_decode_paged_f16" in names and "fa_probe_chain" in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(names) == set(capi.SIGNATURES), "ctypes signatures out of sync with include/*.h"
+
+
+def test_abi_version_and_status_strings(capi):
+    lib = capi.load()
+    assert lib.fa_abi_version() == 1
+    assert lib.fa_status_str(0) == b"ok"
+    assert b"64 or 128" in lib.fa_status_str(capi.STATUS["FA_ERR_HEAD_DIM"])
+    assert b"N must be > 0" == lib.fa_status_str(capi.STATUS["FA_ERR_SEQ_LEN"])
+    assert b"HIP" in lib.fa_status_str(-1)
+
+
+A = 0x10000   # a fake, 16-byte aligned address: never dereferenced by validation
+
+
+@pytest.mark.parametrize("args,code", [
+    ((0, A, A, A, 1, 1, 64, 64), "FA_ERR_NULL_POINTER"),
+    ((A, A, A, 0, 1, 1, 64, 64), "FA_ERR_NULL_POINTER"),
+    ((A, A, A, A, 1, 1, 64, 32), "FA_ERR_HEAD_DIM"),
+    ((A, A, A, A, 1, 1, 64, 96), "FA_ERR_HEAD_DIM"),
+    ((A, A, A, A, 1, 1, 0, 64), "FA_ERR_SEQ_LEN"),
+    ((A, A, A, A, 1, 1, -5, 64), "FA_ERR_SEQ_LEN"),
+    ((A, A, A, A, 0, 1, 64, 64), "FA_ERR_BATCH_HEADS"),
+    ((A, A, A, A, 1, 0, 64, 64), "FA_ERR_BATCH_HEADS"),
+    ((A + 2, A, A, A, 1, 1, 64, 64), "FA_ERR_ALIGNMENT"),
+    ((A, A, A, A, 1, 1, 1 << 25, 128), "FA_ERR_TOO_LARGE"),
+    ((A, A, A, A, 1 << 20, 1 << 20, 128, 64), "FA_ERR_TOO_LARGE"),
+    ((A, A, A, A, 1, 8, 4096, 64), "FA_OK"),
+    ((A, A, A, A, 4, 16, 4096, 128), "FA_OK"),
+    ((A, A, A, A, 1, 1, 1, 64), "FA_OK"),
+])
+def test_validate_fwd(capi, args, code):
+    lib = capi.load()
+    assert lib.fa_validate_fwd(*args) == capi.STATUS[code]
+
+
+def test_fwd_rejects_before_touching_the_device(capi):
+    lib = capi.load()
+    # invalid arguments return their status without any HIP call (no GPU here)
+    assert lib.fa_fwd_f16(A, A, A, A, None, 1, 1, 64, 80, 0, None) == capi.STATUS["FA_ERR_HEAD_DIM"]
+    assert lib.fa_fwd_f16(A, A, A, A, A + 2, 1, 1, 64, 64, 0, None) == capi.STATUS["FA_ERR_ALIGNMENT"]
+    assert lib.fa_fwd_f16(A, 0, A, A, None, 1, 1, 64, 64, 1, None) == capi.STATUS["FA_ERR_NULL_POINTER"]
+
+
+def _dec(**kw):
+    base = dict(q=A, k=A, v=A, pt=A, ctx=A, B=32, H=32, D=128, ps=16, maxp=2048, np_=33000, S=16)
+    base.update(kw)
+    b = base
+    return (b["q"], b["k"], b["v"], b["pt"], b["ctx"], b["B"], b["H"], b["D"], b["ps"], b["maxp"],
+            b["np_"], b["S"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), "FA_OK"),
+    (dict(pt=0), "FA_ERR_NULL_POINTER"),
+    (dict(D=96), "FA_ERR_HEAD_DIM"),
+    (dict(B=0), "FA_ERR_BATCH_HEADS"),
+    (dict(ps=32), "FA_ERR_PAGE_SIZE"),
+    (dict(S=0), "FA_ERR_NUM_SPLITS"),
+    (dict(S=17), "FA_ERR_NUM_SPLITS"),
+    (dict(maxp=0), "FA_ERR_MAX_PAGES"),
+    (dict(np_=0), "FA_ERR_NUM_PAGES"),
+    (dict(k=A + 8), "FA_ERR_ALIGNMENT"),
+    (dict(ctx=A + 2), "FA_ERR_ALIGNMENT"),
+    (dict(H=70000), "FA_ERR_TOO_LARGE"),
+])
+def test_validate_decode(capi, kw, code):
+    lib = capi.load()
+    assert lib.fa_validate_decode(*_dec(**kw)) == capi.STATUS[code]
+
+
+def test_decode_rejects_before_touching_the_device(capi):
+    lib = capi.load()
+    args = _dec(S=20)
+    assert lib.fa_decode_paged_f16(*args, A, A, A, A, None) == capi.STATUS["FA_ERR_NUM_SPLITS"]
+    assert lib.fa_decode_split_f16(*_dec(), 0, A, None) == capi.STATUS["FA_ERR_NULL_POINTER"]
+    assert lib.fa_lse_combine_f32(A, A, 1, 1, 64, 0, A, None, None) == capi.STATUS["FA_ERR_NUM_SPLITS"]
+    assert lib.fa_decode_workspace_floats(32, 32, 128, 16) == 32 * 32 * 16 * 129
+
+
+def test_torch_binding_checks_mirror_reference(fa):
+    """The reference checks is_cuda first (cuda/flash_attn_fa3_db_full.cu:352)."""
+    import torch
+    x = torch.zeros(1, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="Q/K/V must be CUDA tensors"):
+        fa.forward(x, x, x)
+    with pytest.raises(RuntimeError, match="Q/K/V must be CUDA tensors"):
+        fa.forward_only(x, x, x, causal=True)
+    with pytest.raises(RuntimeError, match="must be CUDA tensors"):
+        fa.decode_paged(torch.zeros(1, 1, 64, dtype=torch.half),
+                        torch.zeros(1, 1, 16, 64, dtype=torch.half),
+                        torch.zeros(1, 1, 16, 64, dtype=torch.half),
+                        torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32))
+
+
+def test_package_loads_native_libraries(fa):
+    libs = fa.loaded_libraries()
+    assert any(p.endswith("libfa_mi355x.so") for p in libs)
+    assert any("_fa_torch" in p for p in libs)

@@ -1,0 +1,223 @@
+"""GPU tier: forward parity against the CPU oracle (oracle/naive.py).
+
+Mirrors the reference's contract test (tests/test_fa3_db_full.py:28-82): the
+same config list over both dispatch paths, fp32 and fp16 inputs, the amp
+stress cases, and ``forward_only`` bitwise equal to ``forward``'s O
+(:37-39); plus D=128, causal, the BASELINE configs and determinism.
+
+Tolerances (written out here):
+* amp = 1: O max-abs error <= 2e-3; L relative error <= 1e-4, where the
+  relative error is |L - L_ref| / max(|L_ref|, 1).
+* amp > 1 (the reference's stress extras): the reference's own bound,
+  |O - O_ref| <= 2e-3 * amp + 2e-3 |O_ref| (tests/test_fa3_db_full.py:43), and
+  the same L bound.
+The oracle runs fp32 math on the same fp16-rounded inputs
+(tests/test_fa3_db_full.py:34-35).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import half_cast, make_fwd_inputs, make_ragged_inputs, naive_attention
+
+pytestmark = pytest.mark.gpu
+
+O_ATOL = 2e-3
+L_RTOL = 1e-4
+
+
+def _to_dev(dev, *xs):
+    return [torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in xs]
+
+
+def _check(O, L, Or, Lr, amp=1.0, tag=""):
+    O = O.float().cpu().numpy()
+    o_err = np.abs(O - Or)
+    if amp == 1.0:
+        assert o_err.max() <= O_ATOL, f"{tag} O max-abs {o_err.max():.3e}"
+    else:
+        bound = O_ATOL * amp + 2e-3 * np.abs(Or)
+        assert (o_err <= bound).all(), f"{tag} O err {o_err.max():.3e} (amp {amp})"
+    if L is not None:
+        L = L.cpu().numpy()
+        l_err = np.abs(L - Lr) / np.maximum(np.abs(Lr), 1.0)
+        assert l_err.max() <= L_RTOL, f"{tag} L rel {l_err.max():.3e}"
+    assert np.isfinite(O).all()
+
+
+def _run_case(fa, dev, B, H, N, D, causal=False, amp=1.0, dtype=torch.float32, seed=42):
+    Q, K, V = make_fwd_inputs(B, H, N, D, seed=seed, amp=amp)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    if dtype != torch.float16:
+        # the reference passes fp32 tensors by default; the binding casts to fp16
+        tq, tk, tv = tq.to(dtype), tk.to(dtype), tv.to(dtype)
+    O, L = fa.forward(tq, tk, tv, causal=causal)
+    O2 = fa.forward_only(tq, tk, tv, causal=causal)
+    torch.cuda.synchronize()
+    assert O.dtype == torch.float16 and O.shape == (B, H, N, D)
+    assert L.dtype == torch.float32 and L.shape == (B, H, N)
+    assert torch.equal(O, O2), "forward_only O must equal forward O bitwise"
+    Or, Lr = naive_attention(half_cast(Q), half_cast(K), half_cast(V), causal=causal)
+    _check(O, L, Or, Lr, amp, tag=f"B{B} H{H} N{N} D{D} causal={causal} amp={amp}")
+
+
+# The reference's config list (tests/test_fa3_db_full.py:58-66) for D=64 and D=128.
+REF_CONFIGS = [
+    (1, 1, 64), (1, 1, 128), (2, 8, 512), (1, 1, 1024), (1, 1, 2048), (1, 1, 4096),
+    (1, 1, 1), (1, 1, 2), (1, 1, 7), (1, 1, 31), (1, 1, 33), (1, 1, 63), (1, 1, 127),
+    (1, 1, 4095), (2, 4, 256),
+]
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,H,N", REF_CONFIGS)
+def test_reference_configs(fa, dev, B, H, N, D):
+    _run_case(fa, dev, B, H, N, D)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,H,N", [(1, 1, 1), (1, 1, 7), (1, 1, 64), (1, 1, 127), (1, 2, 128),
+                                   (2, 3, 300), (1, 1, 1024), (1, 2, 4095)])
+def test_causal(fa, dev, B, H, N, D):
+    _run_case(fa, dev, B, H, N, D, causal=True)
+
+
+# The reference's extras (tests/test_fa3_db_full.py:70-75).
+@pytest.mark.parametrize("N,dtype,amp", [
+    (1024, torch.float16, 1.0), (127, torch.float16, 1.0),
+    (2048, torch.float32, 16.0), (4095, torch.float32, 16.0),
+])
+@pytest.mark.parametrize("D", [64, 128])
+def test_reference_extras(fa, dev, N, dtype, amp, D):
+    _run_case(fa, dev, 1, 1, N, D, dtype=dtype, amp=amp)
+
+
+def test_config1_b1_h8_n1024(fa, dev):
+    _run_case(fa, dev, 1, 8, 1024, 64)
+
+
+@pytest.mark.parametrize("N", [2048, 4096])
+def test_config2_headline(fa, dev, N):
+    _run_case(fa, dev, 1, 8, N, 64, dtype=torch.float16)
+
+
+def test_config2_n8192_sampled_heads(fa, dev):
+    """N=8192: full GPU run, oracle on two heads."""
+    B, H, N, D = 1, 8, 8192, 64
+    Q, K, V = make_fwd_inputs(B, H, N, D, seed=42)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O, L = fa.forward(tq, tk, tv)
+    assert torch.equal(O, fa.forward_only(tq, tk, tv))
+    for h in (0, 5):
+        Or, Lr = naive_attention(half_cast(Q[:, h:h + 1]), half_cast(K[:, h:h + 1]),
+                                 half_cast(V[:, h:h + 1]))
+        _check(O[:, h:h + 1], L[:, h:h + 1], Or, Lr, tag=f"N8192 h{h}")
+
+
+def test_config3_causal_b4_h16_n4096_d128(fa, dev):
+    """Config 3: causal B4 H16 N4096 D128, inputs N(0,1)*0.5. The GPU runs the
+    whole batch; the oracle checks three (b, h) heads in full and, for every
+    head, the closed-form first row (O[0] = V[0], L[0] = S[0,0])."""
+    B, H, N, D = 4, 16, 4096, 128
+    Q, K, V = make_fwd_inputs(B, H, N, D, seed=3, amp=0.5)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O, L = fa.forward(tq, tk, tv, causal=True)
+    torch.cuda.synchronize()
+    Oc, Lc = O.cpu(), L.cpu()
+    assert torch.isfinite(Oc.float()).all() and torch.isfinite(Lc).all()
+    assert torch.equal(Oc[:, :, 0], torch.from_numpy(V[:, :, 0]))
+    s00 = (half_cast(Q[:, :, 0]) * half_cast(K[:, :, 0])).sum(-1) / np.sqrt(D)
+    assert np.abs(Lc[:, :, 0].numpy() - s00).max() <= 1e-4 * max(1.0, np.abs(s00).max())
+    for b, h in ((0, 0), (1, 7), (3, 15)):
+        Or, Lr = naive_attention(half_cast(Q[b:b + 1, h:h + 1]), half_cast(K[b:b + 1, h:h + 1]),
+                                 half_cast(V[b:b + 1, h:h + 1]), causal=True)
+        _check(Oc[b:b + 1, h:h + 1], Lc[b:b + 1, h:h + 1], Or, Lr, tag=f"config3 b{b} h{h}")
+
+
+@pytest.mark.parametrize("seed", [7, 8])
+@pytest.mark.parametrize("causal", [False, True])
+def test_config4_ragged_large_logits(fa, dev, seed, causal):
+    """Config 4: B2 H8 D64, N ~ U[1000,5000] not a tile multiple, 5% of Q/K rows at std 3."""
+    N, Q, K, V = make_ragged_inputs(B=2, H=8, D=64, seed=seed)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O, L = fa.forward(tq, tk, tv, causal=causal)
+    assert torch.equal(O, fa.forward_only(tq, tk, tv, causal=causal))
+    Or, Lr = naive_attention(half_cast(Q), half_cast(K), half_cast(V), causal=causal)
+    _check(O, L, Or, Lr, tag=f"ragged N={N} causal={causal}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_golden_fixtures(fa, dev, D):
+    import pathlib
+    gdir = pathlib.Path(__file__).resolve().parent / "golden"
+    for p in sorted(gdir.glob(f"fwd_*_d{D}*.npz")):
+        z = np.load(p)
+        q, k, v = _to_dev(dev, z["q"][None], z["k"][None], z["v"][None])
+        causal = bool(z["causal"])
+        O, L = fa.forward(q, k, v, causal=causal)
+        amp = 3.0 if "amp3" in p.name else 1.0
+        _check(O[0:1], L[0:1], z["o"][None], z["l"][None], amp=amp, tag=p.name)
+
+
+def test_deterministic_repeat(fa, dev):
+    """Repeated launches give bitwise-equal O and L (LDS double-buffer hazards
+    would show up as run-to-run differences)."""
+    Q, K, V = make_fwd_inputs(1, 8, 2048, 64, seed=11)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O0, L0 = fa.forward(tq, tk, tv)
+    for _ in range(5):
+        O1, L1 = fa.forward(tq, tk, tv)
+        assert torch.equal(O0, O1) and torch.equal(L0, L1)
+
+
+def test_key_permutation_invariance(fa, dev):
+    """Permuting K and V rows jointly leaves O within tolerance of the original."""
+    Q, K, V = make_fwd_inputs(1, 2, 1000, 64, seed=12)
+    perm = np.random.default_rng(1).permutation(1000)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O1, L1 = fa.forward(tq, tk, tv)
+    tk2, tv2 = _to_dev(dev, K[:, :, perm], V[:, :, perm])
+    O2, L2 = fa.forward(tq, tk2, tv2)
+    assert (O1.float() - O2.float()).abs().max().item() <= 2e-3
+    assert ((L1 - L2).abs() / L1.abs().clamp_min(1)).max().item() <= 1e-4
+
+
+def test_non_contiguous_and_fp32_inputs(fa, dev):
+    """Arbitrary strides and fp32 are accepted through cast + contiguous
+    (cuda/flash_attn_fa3_db_full.cu:366-368)."""
+    Q, K, V = make_fwd_inputs(1, 2, 96, 64, seed=13)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O_ref, L_ref = fa.forward(tq, tk, tv)
+    tqt = tq.transpose(1, 2).contiguous().transpose(1, 2)   # same values, strided
+    O, L = fa.forward(tqt.float(), tk, tv.float())
+    assert torch.equal(O, O_ref) and torch.equal(L, L_ref)
+
+
+def test_c_abi_direct(fa, capi, dev):
+    """fa_fwd_f16 called through ctypes with raw device pointers and the current stream."""
+    lib = capi.load()
+    Q, K, V = make_fwd_inputs(1, 2, 300, 128, seed=14)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O = torch.empty_like(tq)
+    L = torch.empty(1, 2, 300, device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    st = lib.fa_fwd_f16(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), O.data_ptr(), L.data_ptr(),
+                        1, 2, 300, 128, 1, stream)
+    assert st == 0, lib.fa_status_str(st)
+    torch.cuda.synchronize()
+    O2, L2 = fa.forward(tq, tk, tv, causal=True)
+    assert torch.equal(O, O2) and torch.equal(L, L2)
+
+
+def test_binding_errors_on_gpu(fa, dev):
+    x = torch.zeros(1, 1, 8, 64, device=dev, dtype=torch.half)
+    with pytest.raises(RuntimeError, match="Head dimension must be 64 or 128"):
+        fa.forward(torch.zeros(1, 1, 8, 32, device=dev), torch.zeros(1, 1, 8, 32, device=dev),
+                   torch.zeros(1, 1, 8, 32, device=dev))
+    with pytest.raises(RuntimeError, match="N must be > 0"):
+        z = torch.zeros(1, 1, 0, 64, device=dev)
+        fa.forward(z, z, z)
+    with pytest.raises(RuntimeError, match="same shape as Q"):
+        fa.forward(x, torch.zeros(1, 1, 9, 64, device=dev), x)
+    with pytest.raises(RuntimeError, match="4D"):
+        fa.forward(x[0], x[0], x[0])

@@ -1,0 +1,293 @@
+"""CPU tier: pin the oracle (oracle/naive.py) before trusting it as the checker.
+
+Each oracle function is checked against something it does not share code
+with: the float64 golden fixtures (explicit loops, tests/golden/make_golden.py),
+a pure-Python brute force, closed forms and invariants. The mutation tests at
+the end plant plausible mistakes in copies of the oracle and show that the
+pinning checks catch each of them.
+"""
+import math
+import pathlib
+
+import numpy as np
+import pytest
+
+from oracle import naive as orc
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def _f64(x):
+    return np.asarray(x, dtype=np.float64)
+
+
+# ---------------------------------------------------------------- fixtures
+@pytest.mark.parametrize("name", sorted(p.stem for p in GOLDEN.glob("fwd_*.npz")))
+def test_oracle_matches_golden_fwd(name):
+    z = np.load(GOLDEN / f"{name}.npz")
+    q, k, v = z["q"][None], z["k"][None], z["v"][None]
+    O, L = orc.naive_attention(orc.half_cast(q), orc.half_cast(k), orc.half_cast(v),
+                               causal=bool(z["causal"]))
+    vmax = float(np.abs(z["v"].astype(np.float32)).max())
+    np.testing.assert_allclose(O[0], z["o"], atol=2e-6 * max(vmax, 1.0), rtol=0)
+    np.testing.assert_allclose(L[0], z["l"], atol=2e-5, rtol=2e-6)
+    O64, L64 = orc.naive_attention(q, k, v, causal=bool(z["causal"]), dtype=np.float64)
+    np.testing.assert_allclose(O64[0], z["o"], atol=1e-12)
+    np.testing.assert_allclose(L64[0], z["l"], atol=1e-12)
+
+
+@pytest.mark.parametrize("name", sorted(p.stem for p in GOLDEN.glob("decode_*.npz")))
+def test_oracle_matches_golden_decode(name):
+    z = np.load(GOLDEN / f"{name}.npz")
+    O, L = orc.decode_attention(z["q"], z["k_pool"], z["v_pool"], z["page_table"], z["ctx_lens"],
+                                dtype=np.float64)
+    np.testing.assert_allclose(O, z["o"], atol=1e-12)
+    np.testing.assert_allclose(L, z["l"], atol=1e-12)
+    for S in (1, 2, 3, 16):
+        Os, Ls = orc.split_partials(z["q"], z["k_pool"], z["v_pool"], z["page_table"],
+                                    z["ctx_lens"], S, dtype=np.float64)
+        Oc, Lc = orc.lse_combine(Os, Ls)
+        np.testing.assert_allclose(Oc, z["o"], atol=1e-12)
+        np.testing.assert_allclose(Lc, z["l"], atol=1e-12)
+
+
+def test_oracle_matches_golden_combine():
+    z = np.load(GOLDEN / "combine_b2_s5.npz")
+    O, L = orc.lse_combine(_f64(z["part_o"]), _f64(z["part_lse"]))
+    np.testing.assert_allclose(O, z["o"], atol=1e-12)
+    np.testing.assert_allclose(L, z["l"], atol=1e-12)
+
+
+# ---------------------------------------------------------------- brute force
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N,D", [(1, 8), (5, 16), (23, 64)])
+def test_oracle_vs_bruteforce(N, D, causal):
+    Q, K, V = orc.make_fwd_inputs(1, 2, N, D, seed=N + D)
+    O, L = orc.naive_attention(orc.half_cast(Q), orc.half_cast(K), orc.half_cast(V), causal=causal)
+    for h in range(2):
+        Ob, Lb = orc.attention_bruteforce(_f64(Q[0, h]), _f64(K[0, h]), _f64(V[0, h]), causal)
+        np.testing.assert_allclose(O[0, h], np.array(Ob), atol=2e-6)
+        np.testing.assert_allclose(L[0, h], np.array(Lb), atol=2e-5)
+
+
+# ---------------------------------------------------------------- closed forms
+def test_closed_form_single_key():
+    Q, K, V = orc.make_fwd_inputs(2, 3, 1, 64, seed=1)
+    O, L = orc.naive_attention(Q, K, V, dtype=np.float64)
+    np.testing.assert_array_equal(O, _f64(V))
+    np.testing.assert_allclose(L, (_f64(Q) * _f64(K)).sum(-1) / 8.0, atol=1e-12)
+
+
+def test_closed_form_zero_query():
+    _, K, V = orc.make_fwd_inputs(1, 2, 50, 64, seed=2)
+    Q = np.zeros_like(K)
+    O, L = orc.naive_attention(Q, K, V, dtype=np.float64)
+    np.testing.assert_allclose(O, np.broadcast_to(_f64(V).mean(axis=2, keepdims=True), O.shape),
+                               atol=1e-12)
+    np.testing.assert_allclose(L, np.full(L.shape, math.log(50)), atol=1e-12)
+
+
+def test_closed_form_equal_keys():
+    Q, K, V = orc.make_fwd_inputs(1, 1, 40, 64, seed=3)
+    K[:] = K[:, :, :1, :]
+    O, L = orc.naive_attention(Q, K, V, dtype=np.float64)
+    s = (_f64(Q[0, 0]) @ _f64(K[0, 0, 0])) / 8.0
+    np.testing.assert_allclose(O[0, 0], np.broadcast_to(_f64(V[0, 0]).mean(0), (40, 64)), atol=1e-12)
+    np.testing.assert_allclose(L[0, 0], s + math.log(40), atol=1e-12)
+
+
+def test_closed_form_constant_values():
+    Q, K, _ = orc.make_fwd_inputs(1, 2, 33, 64, seed=4)
+    V = np.full(Q.shape, 0.75, dtype=np.float16)
+    O, _ = orc.naive_attention(Q, K, V, dtype=np.float64)
+    np.testing.assert_allclose(O, 0.75, atol=1e-12)
+
+
+def test_causal_first_and_last_rows():
+    Q, K, V = orc.make_fwd_inputs(1, 2, 30, 64, seed=5)
+    Oc, Lc = orc.naive_attention(Q, K, V, causal=True, dtype=np.float64)
+    On, Ln = orc.naive_attention(Q, K, V, causal=False, dtype=np.float64)
+    np.testing.assert_array_equal(Oc[:, :, 0], _f64(V[:, :, 0]))
+    np.testing.assert_allclose(Lc[:, :, 0], (_f64(Q[:, :, 0]) * _f64(K[:, :, 0])).sum(-1) / 8.0,
+                               atol=1e-12)
+    np.testing.assert_allclose(Oc[:, :, -1], On[:, :, -1], atol=1e-12)
+    np.testing.assert_allclose(Lc[:, :, -1], Ln[:, :, -1], atol=1e-12)
+    # causal row i equals non-causal attention over the prefix [0, i]
+    i = 17
+    Op, Lp = orc.naive_attention(Q[:, :, : i + 1], K[:, :, : i + 1], V[:, :, : i + 1],
+                                 dtype=np.float64)
+    np.testing.assert_allclose(Oc[:, :, i], Op[:, :, i], atol=1e-12)
+    np.testing.assert_allclose(Lc[:, :, i], Lp[:, :, i], atol=1e-12)
+
+
+def test_key_permutation_invariance():
+    Q, K, V = orc.make_fwd_inputs(1, 2, 45, 64, seed=6)
+    perm = np.random.default_rng(0).permutation(45)
+    O1, L1 = orc.naive_attention(Q, K, V, dtype=np.float64)
+    O2, L2 = orc.naive_attention(Q, K[:, :, perm], V[:, :, perm], dtype=np.float64)
+    np.testing.assert_allclose(O1, O2, atol=1e-12)
+    np.testing.assert_allclose(L1, L2, atol=1e-12)
+
+
+def test_softmax_rows_sum_to_one_and_shift_invariance():
+    Q, K, V = orc.make_fwd_inputs(1, 1, 25, 64, seed=8)
+    V1 = np.ones_like(V)
+    O, _ = orc.naive_attention(Q, K, V1, dtype=np.float64)
+    np.testing.assert_allclose(O, 1.0, atol=1e-12)       # rows of P sum to 1
+    # adding a constant to every logit of a row shifts L by that constant
+    Q2 = Q.astype(np.float64)
+    K2 = np.concatenate([K.astype(np.float64), np.ones((1, 1, 25, 1))], axis=-1)
+    Qa = np.concatenate([Q2, np.full((1, 1, 25, 1), 3.0)], axis=-1)
+    Oa, La = orc.naive_attention(Qa, K2, V.astype(np.float64), dtype=np.float64)
+    Ob, Lb = orc.naive_attention(np.concatenate([Q2, np.zeros((1, 1, 25, 1))], -1), K2,
+                                 V.astype(np.float64), dtype=np.float64)
+    np.testing.assert_allclose(Oa, Ob, atol=1e-12)
+    np.testing.assert_allclose(La - Lb, 3.0 / math.sqrt(65), atol=1e-12)
+
+
+# ---------------------------------------------------------------- decode
+def _small_decode(seed=31, B=4, H=3, D=64, ctx=(1, 16, 17, 70)):
+    rng = np.random.default_rng(seed)
+    pages = [(c + 15) // 16 for c in ctx]
+    P = sum(pages)
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((B, max(pages)), np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    q = rng.standard_normal((B, H, D)).astype(np.float16)
+    kp = rng.standard_normal((P, H, 16, D)).astype(np.float16)
+    vp = rng.standard_normal((P, H, 16, D)).astype(np.float16)
+    return q, kp, vp, table, np.array(ctx, np.int32)
+
+
+def test_gather_pages_matches_index_walk():
+    q, kp, vp, table, ctx = _small_decode()
+    for b in range(len(ctx)):
+        for h in range(q.shape[1]):
+            g = orc.gather_pages(kp, table, int(ctx[b]), b, h)
+            walk = np.stack([kp[table[b, j // 16], h, j % 16] for j in range(ctx[b])])
+            np.testing.assert_array_equal(g, walk)
+
+
+def test_decode_equals_naive_over_gathered_keys():
+    q, kp, vp, table, ctx = _small_decode()
+    O, L = orc.decode_attention(q, kp, vp, table, ctx, dtype=np.float64)
+    for b in range(len(ctx)):
+        for h in range(q.shape[1]):
+            k = orc.gather_pages(kp, table, int(ctx[b]), b, h)
+            v = orc.gather_pages(vp, table, int(ctx[b]), b, h)
+            On, Ln = orc.naive_attention(q[b, h][None, None, None], k[None, None],
+                                         v[None, None], dtype=np.float64)
+            np.testing.assert_allclose(O[b, h], On[0, 0, 0], atol=1e-12)
+            np.testing.assert_allclose(L[b, h], Ln[0, 0, 0], atol=1e-12)
+
+
+@pytest.mark.parametrize("S", [1, 2, 5, 16])
+def test_split_combine_equals_unsplit(S):
+    q, kp, vp, table, ctx = _small_decode()
+    O, L = orc.decode_attention(q, kp, vp, table, ctx, dtype=np.float64)
+    Os, Ls = orc.split_partials(q, kp, vp, table, ctx, S, dtype=np.float64)
+    Oc, Lc = orc.lse_combine(Os, Ls)
+    np.testing.assert_allclose(Oc, O, atol=1e-12)
+    np.testing.assert_allclose(Lc, L, atol=1e-12)
+    if S == 1:
+        np.testing.assert_allclose(Os[:, :, 0], O, atol=1e-12)
+
+
+def test_split_bounds_cover_pages_once():
+    for ctx in (1, 15, 16, 17, 100, 32768):
+        for S in (1, 3, 16):
+            b = orc.split_bounds(ctx, 16, S)
+            covered = [p for p0, p1 in b for p in range(p0, p1)]
+            assert covered == list(range((ctx + 15) // 16))
+
+
+def test_combine_empty_splits():
+    Os = np.zeros((1, 1, 4, 8))
+    Ls = np.full((1, 1, 4), -np.inf)
+    O, L = orc.lse_combine(Os, Ls)
+    assert np.all(O == 0) and np.isneginf(L).all()
+    Os[0, 0, 2] = 1.5
+    Ls[0, 0, 2] = 0.3
+    O, L = orc.lse_combine(Os, Ls)
+    np.testing.assert_allclose(O[0, 0], 1.5)
+    np.testing.assert_allclose(L[0, 0], 0.3)
+
+
+def test_decode_meta_is_a_permutation():
+    ctx, table, P = orc.make_decode_meta(B=32, seed=5)
+    pages = (ctx + 15) // 16
+    used = np.concatenate([table[b, :pages[b]] for b in range(32)])
+    assert sorted(used.tolist()) == list(range(P))
+    assert ctx.min() >= 512 and ctx.max() <= 32768
+
+
+def test_ragged_inputs_are_not_tile_multiples():
+    N, Q, K, V = orc.make_ragged_inputs(B=1, H=1, D=64, seed=7)
+    assert 1000 <= N <= 5000 and N % 32 and N % 64 and N % 128
+    assert Q.dtype == np.float16 and Q.shape == (1, 1, N, 64)
+    assert np.abs(Q.astype(np.float32)).max() > 6  # the std-3 rows are present
+
+
+def test_generators_are_deterministic():
+    a = orc.make_fwd_inputs(1, 2, 10, 64, seed=9)
+    b = orc.make_fwd_inputs(1, 2, 10, 64, seed=9)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+
+
+# ---------------------------------------------------------------- mutations
+def _mut_scale(Q, K, V, causal=False, dtype=np.float32):       # 1/D instead of 1/sqrt(D)
+    return orc.naive_attention(Q * np.float32(1 / math.sqrt(Q.shape[-1])), K, V, causal, dtype)
+
+
+def _mut_transpose_v(Q, K, V, causal=False, dtype=np.float32):  # V read as V^T on square heads
+    return orc.naive_attention(Q, K, np.swapaxes(V, -1, -2).copy(), causal, dtype)
+
+
+def _mut_causal_offbyone(Q, K, V, causal=False, dtype=np.float32):  # j < i instead of j <= i
+    if not causal:
+        return orc.naive_attention(Q, K, V, False, dtype)
+    O, L = orc.naive_attention(Q, K, V, True, dtype)
+    Q2 = np.asarray(Q, dtype)
+    O[:, :, 1:], L[:, :, 1:] = orc.naive_attention(Q2[:, :, 1:], K[:, :, :-1], V[:, :, :-1], True, dtype)
+    return O, L
+
+
+def _mut_lse_log2(Q, K, V, causal=False, dtype=np.float32):     # L in log2 instead of ln
+    O, L = orc.naive_attention(Q, K, V, causal, dtype)
+    return O, L / np.float32(math.log(2))
+
+
+@pytest.mark.parametrize("mut", [_mut_scale, _mut_transpose_v, _mut_causal_offbyone, _mut_lse_log2])
+def test_planted_mistakes_are_caught(mut):
+    caught = False
+    for name in sorted(p.stem for p in GOLDEN.glob("fwd_*.npz")):
+        z = np.load(GOLDEN / f"{name}.npz")
+        if mut is _mut_transpose_v and z["q"].shape[1] != z["q"].shape[2]:
+            continue
+        q, k, v = z["q"][None], z["k"][None], z["v"][None]
+        O, L = mut(orc.half_cast(q), orc.half_cast(k), orc.half_cast(v), bool(z["causal"]))
+        vmax = float(np.abs(z["v"].astype(np.float32)).max())
+        if not (np.allclose(O[0], z["o"], atol=2e-6 * max(vmax, 1.0))
+                and np.allclose(L[0], z["l"], atol=2e-5, rtol=2e-6)):
+            caught = True
+    if mut is _mut_transpose_v:
+        # square head (N == D) case built here, checked against brute force
+        Q, K, V = orc.make_fwd_inputs(1, 1, 16, 16, seed=99)
+        O, _ = mut(orc.half_cast(Q), orc.half_cast(K), orc.half_cast(V))
+        Ob, _ = orc.attention_bruteforce(_f64(Q[0, 0]), _f64(K[0, 0]), _f64(V[0, 0]))
+        caught = caught or not np.allclose(O[0, 0], np.array(Ob), atol=2e-6)
+    assert caught
+
+
+def test_planted_combine_mistake_is_caught():
+    z = np.load(GOLDEN / "combine_b2_s5.npz")
+    Os, Ls = _f64(z["part_o"]), _f64(z["part_lse"])
+    # mistake: weights exp(L_s) normalised by count instead of by their sum
+    M = Ls.max(-1, keepdims=True)
+    w = np.where(np.isfinite(Ls), np.exp(Ls - M), 0)
+    bad = (w[..., None] * Os).sum(-2) / np.isfinite(Ls).sum(-1, keepdims=True)
+    assert not np.allclose(bad, z["o"], atol=1e-6)
