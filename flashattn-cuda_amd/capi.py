@@ -32,6 +32,7 @@ SIGNATURES = {
     "fa_probe_mfma32": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp]),
     "fa_probe_mfma16": (C.c_int, [_vp, _vp, _vp, C.c_int, _vp]),
     "fa_probe_tr16_raw": (C.c_int, [_vp, _vp, _vp]),
+    "fa_probe_permlane": (C.c_int, [_vp, _vp, _vp]),
     "fa_probe_frags": (C.c_int, [_vp, _vp, _vp, _i64, _vp]),
     "fa_probe_chain": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
 }

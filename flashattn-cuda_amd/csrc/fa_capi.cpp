@@ -48,7 +48,8 @@ extern "C" int fa_validate_fwd(const void* q, const void* k, const void* v, cons
   if (N <= 0) return FA_ERR_SEQ_LEN;
   if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return FA_ERR_ALIGNMENT;
-  if (N * D > kMaxHeadElems) return FA_ERR_TOO_LARGE;
+  // One head of K or V is addressed through a 32-bit buffer range (bytes).
+  if (N * D * 2 > kMaxHeadElems) return FA_ERR_TOO_LARGE;
   if (B > kMaxGrid / H) return FA_ERR_TOO_LARGE;
   const int64_t bh = B * H;
   const int64_t num_qb = (N + 127) / 128;

@@ -47,6 +47,7 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
   const int dq = lane & 3;     // quarter of D
 
   if (tid == 0) sh_bad = 0;
+  __syncthreads();
 
   int ctx = ctx_lens[b];
   bool bad = false;

@@ -11,8 +11,10 @@
 //   * one workgroup = 4 waves = 128 query rows of one (b, h); each wave owns
 //     32 rows; a 1-D grid with an XCD-aware remap keeps the query blocks of a
 //     head on one XCD so its K/V stay in that XCD's L2;
-//   * K/V advance in 64-key tiles through two LDS stages; the next tile is
-//     fetched into registers while the current one is consumed;
+//   * K/V advance in 64-key tiles through two LDS stages (two separate LDS
+//     objects, so the compiler can see that reads of one stage never alias
+//     the DMA into the other); the next tile is copied global -> LDS by
+//     buffer_load ... lds while the current one is consumed;
 //   * S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16_f16 (fa_tile.hpp);
 //   * softmax state per lane; the running max is only raised when a new
 //     block max exceeds it by more than 2^8 (P <= 256 stays exact in fp32
@@ -32,6 +34,7 @@ namespace fa {
 constexpr int kBR = 128;   // query rows per workgroup
 constexpr int kBC = 64;    // keys per tile
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 // Workgroup g of `total` lands on XCD g % 8. Map it to a logical tile index
@@ -50,9 +53,10 @@ fa_fwd_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int KSTEPS = D / 16;                  // QK k-steps
   constexpr int DB = D / 32;                      // O^T d-blocks
   constexpr int TILE = kBC * D * 2;               // bytes of one K or V tile
-  constexpr int CPR = D / 8;                      // 16-byte chunks per row
-  constexpr int LOADS = kBC * CPR / kThreads;     // chunks per thread per tile
-  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * TILE];
+  constexpr int BLOCKS = TILE / 1024;             // 1 KiB DMA blocks per tile
+  constexpr int LOADS = BLOCKS / kWaves;          // DMA blocks per wave per tile
+  __shared__ __attribute__((aligned(1024))) char smem0[2 * TILE];   // stage 0: K|V
+  __shared__ __attribute__((aligned(1024))) char smem1[2 * TILE];   // stage 1: K|V
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -65,7 +69,7 @@ fa_fwd_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
 
   const size_t head = (size_t)bh * N * D;
-  const f16* Qh = Q + head;
+  const int head_bytes = N * D * 2;
   const f16* Kh = K + head;
   const f16* Vh = V + head;
 
@@ -74,50 +78,44 @@ fa_fwd_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int qrow = row_w + (lane & 31);
 
   // Q^T as the B operand of S^T = K Q^T, kept in registers for the whole loop.
+  // Buffer loads return zero for rows >= N.
   f16x8 qf[KSTEPS];
+  {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + head, head_bytes);
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) {
-    if (FULL || qrow < N) {
-      qf[kk] = *reinterpret_cast<const f16x8*>(Qh + (size_t)qrow * D + 16 * kk + 8 * hi);
-    } else {
-      qf[kk] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(
+          rq, (uint32_t)(qrow * D + 16 * kk + 8 * hi) * 2, 0, 0);
+      qf[kk] = __builtin_bit_cast(f16x8, x);
     }
   }
 
+  // Tile loads go global -> LDS directly. Each wave fills LOADS 1 KiB blocks
+  // of the K tile and of the V tile; lane l writes bytes [16 l, 16 l + 16) of a
+  // block, so the swizzle is applied by choosing which global chunk it fetches.
+  uint32_t koff[LOADS], voff[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int o = (wave * LOADS + i) * 1024 + 16 * lane;
+    const int r = o / (2 * D);
+    const int slot = (o % (2 * D)) / 16;
+    koff[i] = (uint32_t)(r * 2 * D + (slot ^ k_swz<D>(r)) * 16);
+    voff[i] = (uint32_t)(r * 2 * D + (slot ^ v_swz<D>(r)) * 16);
+  }
+  auto issue = [&](int t, char* stage) {
+    const int done = t * TILE;
+    const int bytes = FULL ? TILE : min(TILE, head_bytes - done);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(Kh) + done, bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(Vh) + done, bytes);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      dma16(rk, stage + (wave * LOADS + i) * 1024, koff[i]);
+      dma16(rv, stage + TILE + (wave * LOADS + i) * 1024, voff[i]);
+    }
+  };
+
   const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
   const int n_tiles = (kv_end + kBC - 1) / kBC;
-
-  u32x4 kst[LOADS], vst[LOADS];
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int id = tid + kThreads * i;
-      const int r = id / CPR, cc = id % CPR;
-      const int key = t * kBC + r;
-      if (FULL || key < N) {
-        kst[i] = *reinterpret_cast<const u32x4*>(Kh + (size_t)key * D + cc * 8);
-        vst[i] = *reinterpret_cast<const u32x4*>(Vh + (size_t)key * D + cc * 8);
-      } else {
-        kst[i] = u32x4{0, 0, 0, 0};
-        vst[i] = u32x4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto sstore = [&](int stage) {
-    char* ks = smem + stage * 2 * TILE;
-    char* vs = ks + TILE;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int id = tid + kThreads * i;
-      const int r = id / CPR, cc = id % CPR;
-      *reinterpret_cast<u32x4*>(ks + k_off<D>(r, cc)) = kst[i];
-      *reinterpret_cast<u32x4*>(vs + v_off<D>(r, cc)) = vst[i];
-    }
-  };
-
-  gload(0);
-  sstore(0);
-  __syncthreads();
 
   f32x16 o[DB];
 #pragma unroll
@@ -125,83 +123,87 @@ fa_fwd_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int stage = t & 1;
-    const bool more = t + 1 < n_tiles;
-    if (more) gload(t + 1);
-    const char* ks = smem + stage * 2 * TILE;
+  auto compute = [&](int t, const char* ks) {
     const char* vs = ks + TILE;
     const int key0 = t * kBC;
-    const bool active = !CAUSAL || key0 <= row_w + 31;   // wave-uniform
-    if (active) {
-      f32x16 s[2];
+    if (CAUSAL && key0 > row_w + 31) return;   // wave-uniform: tile fully masked
+    f32x16 s[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = f32x16{};
+    for (int kb = 0; kb < 2; ++kb) s[kb] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          s[kb] = mfma32(load_k_frag<D>(ks, kb, kk, lane), qf[kk], s[kb]);
-        }
-      }
-      const bool need_mask = (!FULL && key0 + kBC > N) || (CAUSAL && key0 + kBC - 1 > row_w);
-      if (need_mask) {
+    for (int kk = 0; kk < KSTEPS; ++kk) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + st_key(kb, r, lane);
-            const bool dead = (!FULL && key >= N) || (CAUSAL && key > qrow);
-            if (dead) s[kb][r] = -INFINITY;
-          }
-        }
-      }
-      float mx = s[0][0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
-      mx = fmaxf(mx, xor32(mx));
-      const float mt = mx * c;
-      const bool raise = mt > m_run + kRescaleThreshold;
-      if (__any(raise)) {
-        const float m_new = raise ? mt : m_run;
-        const float alpha = (m_new == m_run) ? 1.f : exp2_hw(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db] *= alpha;
-        m_run = m_new;
-      }
-      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-      float rs = 0.f;
+      for (int kb = 0; kb < 2; ++kb) s[kb] = mfma32(load_k_frag<D>(ks, kb, kk, lane), qf[kk], s[kb]);
+    }
+    const bool need_mask = (!FULL && key0 + kBC > N) || (CAUSAL && key0 + kBC - 1 > row_w);
+    if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = exp2_hw(fmaf(s[kb][r], c, -m_use));
-          s[kb][r] = p;
-          rs += p;
-        }
-      }
-      l_run += rs;
-      f16x8 pf[4];
-      pf[0] = pack_p(s[0], 0);
-      pf[1] = pack_p(s[0], 1);
-      pf[2] = pack_p(s[1], 0);
-      pf[3] = pack_p(s[1], 1);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          o[db] = mfma32(load_v_frag<D>(vs, j, db, lane), pf[j], o[db]);
+          const int key = key0 + st_key(kb, r, lane);
+          const bool dead = (!FULL && key >= N) || (CAUSAL && key > qrow);
+          if (dead) s[kb][r] = -INFINITY;
         }
       }
     }
-    if (more) sstore(stage ^ 1);
+    float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
+    mx = max_xor32(mx);
+    const float mt = mx * c;
+    const bool raise = mt > m_run + kRescaleThreshold;
+    if (__any(raise)) {
+      const float m_new = raise ? mt : m_run;
+      const float alpha = (m_new == m_run) ? 1.f : exp2_hw(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = exp2_hw(fmaf(s[kb][r], c, -m_use));
+        s[kb][r] = p;
+        rs += p;
+      }
+    }
+    l_run += rs;
+    const f16x8 pf[4] = {pack_p(s[0], 0), pack_p(s[0], 1), pack_p(s[1], 0), pack_p(s[1], 1)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] = mfma32(load_v_frag<D>(vs, j, db, lane), pf[j], o[db]);
+    }
+  };
+
+  // Two LDS stages; the loop is unrolled by two so stage offsets are constants.
+  char* st0 = smem0;
+  char* st1 = smem1;
+  issue(0, st0);
+  wait_vmem();
+  __syncthreads();
+  for (int t = 0; t < n_tiles; t += 2) {
+    if (t + 1 < n_tiles) issue(t + 1, st1);
+    compute(t, st0);
+    wait_vmem();
     __syncthreads();
+    if (t + 1 < n_tiles) {
+      if (t + 2 < n_tiles) issue(t + 2, st0);
+      compute(t + 1, st1);
+      wait_vmem();
+      __syncthreads();
+    }
   }
 
   // Epilogue: combine the two half-rows, normalise, store O (and L).
-  const float l_tot = l_run + xor32(l_run);
+  const float l_tot = sum_xor32(l_run);
   if (FULL || qrow < N) {
     const float inv = 1.f / l_tot;
     f16* orow = O + head + (size_t)qrow * D;

@@ -54,8 +54,21 @@ __global__ void probe_tr16_raw_kernel(const uint16_t* in, uint16_t* out) {
   for (int i = 0; i < 4; ++i) lds[4 * l + i] = in[4 * l + i];
   __syncthreads();
   f16x4 v = lds_read_tr16(reinterpret_cast<const char*>(lds) + 8 * l);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) out[4 * l + e] = __builtin_bit_cast(uint16_t, v[e]);
+  // Store the vector whole: extracting elements through __builtin_bit_cast was
+  // observed to be miscompiled (all four lanes of the vector read element 0).
+  *reinterpret_cast<f16x4*>(out + 4 * l) = v;
+}
+
+// v_permlane32_swap_b32 with both operands x = in[l]: out[l] = r0, out[64+l] = r1,
+// plus the max/sum helpers the forward kernel uses: out[128+l], out[192+l].
+__global__ void probe_permlane_kernel(const float* in, float* out) {
+  const int l = threadIdx.x;
+  const float x = in[l];
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  out[l] = __uint_as_float(r[0]);
+  out[64 + l] = __uint_as_float(r[1]);
+  out[128 + l] = max_xor32(x);
+  out[192 + l] = sum_xor32(x);
 }
 
 // Stores a [64][D] tile with the forward kernel's K and V layouts, then reads
@@ -146,6 +159,12 @@ extern "C" int fa_probe_tr16_raw(const void* in, void* out, void* stream) {
   if (!in || !out) return 1;
   hipLaunchKernelGGL(fa::probe_tr16_raw_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
                      (const uint16_t*)in, (uint16_t*)out);
+  return finish();
+}
+
+extern "C" int fa_probe_permlane(const float* in, float* out, void* stream) {
+  if (!in || !out) return 1;
+  hipLaunchKernelGGL(fa::probe_permlane_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, in, out);
   return finish();
 }
 

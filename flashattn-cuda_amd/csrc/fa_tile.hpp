@@ -46,10 +46,34 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // log2(x) on v_log_f32.
 __device__ __forceinline__ float log2_hw(float x) { return __builtin_amdgcn_logf(x); }
 
-// Value of lane (l ^ 32).
-__device__ __forceinline__ float xor32(float x) {
-  return __shfl_xor(x, 32, 64);
+// v_permlane32_swap_b32 with both operands x: element 0 of the result holds,
+// in lanes 32..63, x of lane l-32 (lanes 0..31 keep x); element 1 holds, in
+// lanes 0..31, x of lane l+32 (lanes 32..63 keep x). So {r0, r1} is
+// {x[l], x[l^32]} in some order in every lane.
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+
+__device__ __forceinline__ float sum_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Raw buffer resource over `bytes` bytes at `base`: loads at offsets beyond
+// `bytes` return zero instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// 16 bytes per lane from global (rsrc + voffset) straight into LDS at
+// lds + 16*lane (the LDS base is wave-uniform).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
 // LDS tile layouts. A K or V tile is BC rows (keys) x D fp16, row stride 2*D
@@ -58,22 +82,29 @@ __device__ __forceinline__ float xor32(float x) {
 // operand reads below hit distinct LDS banks within each 16-lane group.
 // ---------------------------------------------------------------------------
 template <int D>
-__device__ __forceinline__ int k_slot(int r, int c) {
+__device__ __forceinline__ int k_swz(int r) {
   if constexpr (D == 64) {
-    return c ^ ((r >> 1) & 7);
+    return (r >> 1) & 7;
   } else {
-    return c ^ (r & 15);
+    return r & 15;
   }
 }
 
 template <int D>
-__device__ __forceinline__ int v_slot(int r, int c) {
+__device__ __forceinline__ int v_swz(int r) {
   if constexpr (D == 64) {
-    return c ^ (((r >> 1) & 1) << 2);
+    return ((r >> 1) & 1) << 2;
   } else {
-    return c ^ ((r & 3) << 2);
+    return (r & 3) << 2;
   }
 }
+
+// XOR swizzles are involutions: slot = c ^ swz(r) and c = slot ^ swz(r).
+template <int D>
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ k_swz<D>(r); }
+
+template <int D>
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ v_swz<D>(r); }
 
 template <int D>
 __device__ __forceinline__ int k_off(int r, int c) { return r * (2 * D) + k_slot<D>(r, c) * 16; }

@@ -196,6 +196,15 @@ torch::Tensor probe_tr16_raw(torch::Tensor in) {
   return out;
 }
 
+torch::Tensor probe_permlane(torch::Tensor in) {
+  TORCH_CHECK(in.is_cuda() && in.numel() == 64 && in.scalar_type() == torch::kFloat);
+  auto ic = in.contiguous();
+  auto out = torch::empty({4, 64}, in.options());
+  check_status(fa_probe_permlane(ic.data_ptr<float>(), out.data_ptr<float>(), current_stream(in)),
+               "fa_probe_permlane");
+  return out;
+}
+
 std::vector<torch::Tensor> probe_frags(torch::Tensor tile) {
   TORCH_CHECK(tile.is_cuda() && tile.dim() == 2 && tile.size(0) == 64 &&
               (tile.size(1) == 64 || tile.size(1) == 128) && tile.scalar_type() == torch::kHalf);
@@ -238,6 +247,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("probe_mfma32", &probe_mfma32);
   m.def("probe_mfma16", &probe_mfma16);
   m.def("probe_tr16_raw", &probe_tr16_raw);
+  m.def("probe_permlane", &probe_permlane);
   m.def("probe_frags", &probe_frags);
   m.def("probe_chain", &probe_chain);
   m.def("abi_version", &fa_abi_version);

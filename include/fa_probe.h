@@ -28,6 +28,11 @@ int fa_probe_mfma16(const void* a, const void* b, float* c, int variant, void* s
  * offset 8*l and writes its 4 halves to out[4*l .. 4*l+3]. */
 int fa_probe_tr16_raw(const void* in, void* out, void* stream);
 
+/* v_permlane32_swap_b32 on x = in[0..63]: out[0..63] and out[64..127] are the
+ * two results; out[128..191] = max(x[l], x[l^32]), out[192..255] = x[l] + x[l^32]
+ * through the forward kernel's helpers. */
+int fa_probe_permlane(const float* in, float* out, void* stream);
+
 /* Stores a [64][D] fp16 tile with the forward kernel's K and V LDS layouts and
  * dumps every operand fragment the kernel reads:
  *   kout [2][D/16][64][8], vout [4][D/32][64][8] fp16. D in {64, 128}. */

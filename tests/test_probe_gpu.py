@@ -30,6 +30,17 @@ def test_mfma16_layout(fa, dev):
     assert (bad - ref).abs().max().item() > 0.5
 
 
+def test_permlane32_swap(fa, dev):
+    x = torch.arange(64, dtype=torch.float32) * 1.5 - 7
+    out = fa.probe.probe_permlane(x.to(dev)).cpu()
+    partner = x.view(2, 32).flip(0).reshape(-1)
+    r0 = torch.where(torch.arange(64) < 32, x, partner)
+    r1 = torch.where(torch.arange(64) < 32, partner, x)
+    assert torch.equal(out[0], r0) and torch.equal(out[1], r1)
+    assert torch.equal(out[2], torch.maximum(x, partner))
+    assert torch.equal(out[3], x + partner)
+
+
 def test_ds_read_tr16_semantics(fa, dev):
     """Lane s of each 16-lane group reading 8 bytes at 8*l receives the 4 halves
     at element offsets 64*g + 16*e + s (a column of a 4x16 row-major block)."""
