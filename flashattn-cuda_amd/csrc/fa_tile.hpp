@@ -66,14 +66,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-// 16 bytes per lane from global (rsrc + voffset) straight into LDS at
-// lds + 16*lane (the LDS base is wave-uniform).
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
-                                           voffset, 0, 0, 0);
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// 16 bytes per lane from global (rsrc + voffset) straight into LDS at byte
+// lds + 16*lane (lds is wave-uniform). Written as inline assembly so the
+// compiler does not treat it as an LDS store: it would otherwise wait for
+// every DMA in flight before any LDS read it cannot prove disjoint. The
+// kernels order these copies themselves (s_waitcnt vmcnt(0) + barrier before
+// the data is read), and nothing else in them uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(r)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(0) through the builtin, so the compiler also knows that its
+// own vector-memory loads issued before this point have completed (gfx9
+// encoding: vmcnt bits [3:0] and [15:14] = 0, expcnt 7, lgkmcnt 15).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // ---------------------------------------------------------------------------
 // LDS tile layouts. A K or V tile is BC rows (keys) x D fp16, row stride 2*D
