@@ -34,6 +34,33 @@ REF_TFLOPS_N4096 = 34.36 / 0.8726   # reference db_full forward()+L, RTX 4060 Ti
 METRIC = "FA fwd TFLOP/s & % FP16 MFMA peak at B1 H8 N4096 D64; decode GB/s"
 
 
+def kernel_name(variant, D, causal=False, write_l=True, full=True):
+    """Template instance of the forward kernel behind a variant code."""
+    c, w, f = (str(x).lower() for x in (causal, write_l, full))
+    if variant == 204:
+        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4>"
+    if variant > 100:
+        return f"fa_fwd_pipe_kernel<{D},{c},{w},{f},{variant % 10},{(variant - 100) // 10}>"
+    return f"fa_fwd_split_kernel<{D},{c},{w},{f},{variant // 10},{variant % 10}>"
+
+
+def pmc_traffic(kernel):
+    """HBM bytes per launch of `kernel` at the headline shape, from the committed
+    rocprofv3 counter summary (FETCH_SIZE x copy factor + WRITE_SIZE); None if
+    the summary does not cover this kernel."""
+    path = ROOT / "profiles" / "fa_fwd_pmc_b1h8n4096d64.md"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if ":" in line and line.strip().startswith(("kernel:", "traffic_bytes_per_launch:")):
+            key, val = line.split(":", 1)
+            vals[key.strip()] = val.strip()
+    if vals.get("kernel") != kernel or "traffic_bytes_per_launch" not in vals:
+        return None
+    return float(vals["traffic_bytes_per_launch"])
+
+
 def fwd_flops(B, H, N, D, causal=False):
     f = 4.0 * B * H * N * N * D
     return f / 2 if causal else f
@@ -202,6 +229,7 @@ def main():
     ms_step = start.elapsed_time(stop) / args.steps
     flops = fwd_flops(B, H, N, D)
     tflops = flops / (ms_step * 1e-3) / 1e12
+    kname = kernel_name(int(fa.probe.probe_default_variant(D)), D)
 
     out = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -217,9 +245,11 @@ def main():
         "wall_s_timed_region": round(wall_s, 4),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-                     "traffic": None,
-                     "kernel": "fa_fwd_kernel<64,false,true,true>",
-                     "algorithmic_flops_per_launch": flops},
+                     "traffic": pmc_traffic(kname),
+                     "kernel": kname,
+                     "algorithmic_flops_per_launch": flops,
+                     "algorithmic_hbm_bytes_per_launch": 3 * B * H * N * D * 2 + B * H * N * D * 2
+                                                         + B * H * N * 4},
     }
 
     if args.only == "all":

@@ -115,64 +115,55 @@ struct RowBlock {
     }
   }
 
-  // The same products with the operand loads kept one k-step ahead of the
-  // MFMAs and nothing moved across steps: bounds the live operand registers
-  // (for kernels that run several waves per SIMD, whose other waves hide the
-  // LDS latency).
-  template <int NB>
-  __device__ __forceinline__ void qk_lean(const char* ks, int kb0, f32x16 (&s)[NB]) const {
-    f16x8 a[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      s[b] = f32x16{};
-      a[b] = load_k_frag<D>(ks, kb0 + b, 0, lane);
-    }
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      f16x8 n[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) n[b] = (kk + 1 < KSTEPS) ? load_k_frag<D>(ks, kb0 + b, kk + 1, lane) : a[b];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) s[b] = mfma32(a[b], qf[kk], s[b]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int b = 0; b < NB; ++b) a[b] = n[b];
-    }
-  }
-
   // Key of register r in block kb is key0 + 4 hi + kofs(kb, r) with a
   // compile-time kofs, so each test compares that constant against one
-  // per-tile lane value (no per-register key arrays kept live).
+  // per-tile lane limit (no per-register key arrays kept live). Keys >= N and,
+  // if CAUSAL, keys > the lane's query row get -inf.
   template <int NB>
-  __device__ __forceinline__ void mask(int t, int kb0, f32x16 (&s)[NB]) const {
-    const int key0 = t * kBC;
-    const bool need = (!FULL && key0 + kBC > N) || (CAUSAL && key0 + kBC - 1 > row_w);
-    if (need) {
-      const int lane_key = key0 + 4 * hi;
-      const int n_lim = N - lane_key;      // dead if kofs >= n_lim
-      const int c_lim = qrow - lane_key;   // dead if kofs >  c_lim
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kofs = st_key(kb0 + b, r, 0);
-          const bool dead = (!FULL && kofs >= n_lim) || (CAUSAL && kofs > c_lim);
-          if (dead) s[b][r] = -INFINITY;
-        }
-      }
-    }
-  }
-
-  // p = 2^(s c - m) into p (which may alias s); returns this lane's sum.
-  template <int NB>
-  __device__ __forceinline__ float expo(const f32x16 (&s)[NB], f32x16 (&p)[NB], float m) const {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  __device__ __forceinline__ void mask_all(int t, int kb0, f32x16 (&s)[NB]) const {
+    const int lane_key = t * kBC + 4 * hi;
+    int lim = N - 1 - lane_key;                    // live iff kofs <= lim
+    if (CAUSAL) lim = min(lim, qrow - lane_key);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[b][r] = exp2_hw(fmaf(s[b][r], c, -m));
-        acc[r & 3] += p[b][r];
+        if (st_key(kb0 + b, r, 0) > lim) s[b][r] = -INFINITY;
+      }
+    }
+  }
+
+  // mask_all for the tiles that need it (the last tile of a ragged N, the
+  // tiles crossing the causal diagonal); a wave-uniform branch skips the rest.
+  template <int NB>
+  __device__ __forceinline__ void mask(int t, int kb0, f32x16 (&s)[NB]) const {
+    const int key0 = t * kBC;
+    const bool need = (!FULL && key0 + kBC > N) || (CAUSAL && key0 + kBC - 1 > row_w);
+    if (need) mask_all<NB>(t, kb0, s);
+  }
+
+  // p = 2^(s c - m), rounded to fp16 and packed as the B operands (P^T) of
+  // the PV k-steps: two per 32-key block, in S^T register order. Returns this
+  // lane's sum of the fp32 values (the normaliser keeps fp32 accuracy even
+  // for short rows, where fp16 rounding of P would not average out).
+  template <int NB>
+  __device__ __forceinline__ float expo_pack(const f32x16 (&s)[NB], f16x8 (&pf)[2 * NB],
+                                             float m) const {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f16x2 x[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = 8 * h + 2 * q;
+          const float e0 = exp2_hw(fmaf(s[b][r], c, -m));
+          const float e1 = exp2_hw(fmaf(s[b][r + 1], c, -m));
+          acc[q] += e0 + e1;
+          x[q] = cvt2(e0, e1);
+        }
+        pf[2 * b + h] = f16x8{x[0][0], x[0][1], x[1][0], x[1][1], x[2][0], x[2][1], x[3][0], x[3][1]};
       }
     }
     return (acc[0] + acc[1]) + (acc[2] + acc[3]);
@@ -199,44 +190,22 @@ struct RowBlock {
 
   __device__ __forceinline__ float m_safe() const { return (m_run == -INFINITY) ? 0.f : m_run; }
 
-  // B operands (P^T) of the PV k-steps of the blocks: two per block.
+  // Slow path of the softmax: some lane's tile sum at the running max left
+  // the fp16-safe range (or is not finite: first tile, m_run = -inf). Raise
+  // the max to the tile's row max and redo the exponentials.
   template <int NB>
-  static __device__ __forceinline__ void pack(const f32x16 (&p)[NB], f16x8 (&pf)[2 * NB]) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      pf[2 * b] = pack_p(p[b], 0);
-      pf[2 * b + 1] = pack_p(p[b], 1);
-    }
+  __device__ __forceinline__ float rescue(const f32x16 (&s)[NB], f16x8 (&pf)[2 * NB]) {
+    raise_max<NB>(s);
+    return expo_pack<NB>(s, pf, m_safe());
   }
 
-  // Softmax of the blocks, keeping the scores (the pipelined kernel cannot
-  // reread K(t): its LDS stage is already being refilled).
+  // Softmax of the blocks into packed P; the scores stay intact for the
+  // slow path.
   template <int NB>
   __device__ __forceinline__ void softmax_keep(const f32x16 (&s)[NB], f16x8 (&pf)[2 * NB]) {
-    f32x16 p[NB];
-    float rs = expo<NB>(s, p, m_run);
-    if (!__all(rs <= kSumLimit)) {
-      raise_max<NB>(s);
-      rs = expo<NB>(s, p, m_safe());
-    }
+    float rs = expo_pack<NB>(s, pf, m_run);
+    if (!__all(rs <= kSumLimit)) rs = rescue<NB>(s, pf);
     l_run += rs;
-    pack<NB>(p, pf);
-  }
-
-  // Softmax in place; on the rare slow path the scores are recomputed from
-  // the K tile still resident at ks.
-  template <int NB>
-  __device__ __forceinline__ void softmax_inplace(f32x16 (&s)[NB], f16x8 (&pf)[2 * NB],
-                                                  const char* ks, int t, int kb0) {
-    float rs = expo<NB>(s, s, m_run);
-    if (!__all(rs <= kSumLimit)) {
-      qk_lean<NB>(ks, kb0, s);
-      mask<NB>(t, kb0, s);
-      raise_max<NB>(s);
-      rs = expo<NB>(s, s, m_safe());
-    }
-    l_run += rs;
-    pack<NB>(s, pf);
   }
 
   // O^T += V^T P^T over the PV k-steps of the blocks.
@@ -247,21 +216,6 @@ struct RowBlock {
 #pragma unroll
       for (int db = 0; db < DB; ++db)
         o[db] = mfma32(load_v_frag<D>(vs, 2 * kb0 + j, db, lane), pf[j], o[db]);
-    }
-  }
-
-  // PV with one (k-step, d-block) operand load in flight ahead of its MFMA.
-  template <int NB>
-  __device__ __forceinline__ void pv_lean(const char* vs, int kb0, const f16x8 (&pf)[2 * NB]) {
-    f16x8 a = load_v_frag<D>(vs, 2 * kb0, 0, lane);
-#pragma unroll
-    for (int i = 0; i < 2 * NB * DB; ++i) {
-      const int j = i / DB, db = i % DB;
-      f16x8 n = a;
-      if (i + 1 < 2 * NB * DB) n = load_v_frag<D>(vs, 2 * kb0 + (i + 1) / DB, (i + 1) % DB, lane);
-      o[db] = mfma32(a, pf[j], o[db]);
-      __builtin_amdgcn_sched_barrier(0);
-      a = n;
     }
   }
 
@@ -498,18 +452,40 @@ fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   rb.template finish<WRITE_L>(O + head, L + (size_t)bh * N);
 }
 
+// f(integral_constant<int, I>) for I = B .. E-1, expanded at compile time
+// (a fixed instruction schedule must not depend on the loop unroller).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Pipelined kernel: 4*KSPLIT waves; wave w is row group w % 4 and key slice
-// w / 4 (as in the split kernel), and tiles advance in groups of KSPLIT. Step
-// g issues the MFMAs of two different tiles of the wave's slice, QK of its
+// w / 4 (as in the split kernel), and tiles advance in groups of KSPLIT.
+//
+// Step g issues the MFMAs of two other tiles of the wave's slice, QK of its
 // tile in group g+1 and PV of its tile in group g-1, while the VALU computes
-// the softmax of its tile in group g: none of the step's MFMAs depends on its
-// VALU work, so matrix cores and VALU run side by side within one wave, and
-// with KSPLIT = 2 a second wave shares each SIMD. K therefore runs two groups
-// ahead of V: step g reads K(g+1) and V(g-1), and its DMA fills K(g+2) and
-// V(g) into the stages those reads do not touch.
+// the softmax of its tile in group g. None of the step's MFMAs depends on its
+// VALU work, so the step is written as a fixed schedule of chunks, each one
+// MFMA + the LDS reads of the MFMA PF places later + a slice of the softmax,
+// fenced by sched_barrier: the matrix core runs while the same wave computes
+// exponentials, and a 64-key step costs about max(MFMA, VALU), not the sum.
+//
+// K and V tiles go through rings of RING LDS slots each; K(x) and V(x) live
+// in slot x % RING. Step g reads K(g+1) and V(g-1). MID_BACK MFMAs before its
+// end, once all its reads are done, the step waits for its own copies of
+// K(g+2) and V(g), meets the other waves at the barrier, issues the copies of
+// K(g+1+RING) (into the slot of K(g+1)) and V(g+RING-1) (slot of V(g-1)), and
+// reads the first operands of step g+1, so the next step starts with its
+// operands in registers and each copy has about RING-1 steps to land. Copies
+// of tiles past the end are still issued, with an empty buffer range (they
+// write zeros and read nothing), so every wave issues the same number per
+// step and the vmcnt waits are exact.
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT>
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int RING>
 __global__ void __launch_bounds__(256 * KSPLIT)
 fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, f16* __restrict__ O,
@@ -517,12 +493,23 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int TILE = kBC * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int WAVES = kRowGroups * KSPLIT;
-  constexpr int LOADS = KSPLIT * BLOCKS / WAVES;          // blocks per wave per group
-  constexpr int GROUP = KSPLIT * TILE;                    // bytes of one K or V stage
-  static_assert(4 * GROUP <= 160 * 1024, "stages exceed the 160 KiB LDS");
+  constexpr int LOADS = KSPLIT * BLOCKS / WAVES;          // blocks per wave per group (K or V)
+  constexpr int GROUP = KSPLIT * TILE;                    // bytes of one K or V slot
+  constexpr int PER_STEP = 2 * LOADS;                     // copies per wave per step
+  static_assert(RING >= 2 && RING <= 4, "two to four slots");
+  static_assert(2 * RING * GROUP <= 160 * 1024, "slots exceed the 160 KiB LDS");
   using RB = RowBlock<D, CAUSAL, FULL>;
   static_assert((KSPLIT - 1) * (2 + 16 * RB::DB) * 64 * 4 <= GROUP, "merge area too small");
-  __shared__ __attribute__((aligned(1024))) char smem[4 * GROUP];   // [K0 | K1 | V0 | V1]
+  constexpr int DB = RB::DB;
+  constexpr int NMM = D / 8;     // MFMAs of QK (2 blocks x D/16 k-steps) = of PV (4 x DB)
+  constexpr int PF = D == 64 ? 8 : 4;   // operand prefetch distance, in MFMAs
+  constexpr int MID_BACK = 2;    // the step barrier sits this many MFMAs before the end
+  constexpr int NSLOT = 17;      // softmax slots of a step (16 value pairs, pipelined)
+  // Step 0's PF first operands are all of its own; every read of a step is
+  // issued before its barrier.
+  static_assert(PF <= NMM && MID_BACK >= 1 && MID_BACK <= PF, "bad step schedule");
+  // K slots at [0, RING) * GROUP, V slots at [RING, 2 RING) * GROUP.
+  __shared__ __attribute__((aligned(1024))) char smem[2 * RING * GROUP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -553,100 +540,198 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     blk_of[i] = blk % BLOCKS;
     dma_offsets<D>(blk_of[i], lane, koff[i], voff[i]);
   }
+  // Per-lane offsets of the operand fragments within a tile.
+  int koffs[D / 16], voffs[DB];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) koffs[kk] = k_frag_off<D>(kk, lane);
+#pragma unroll
+  for (int db = 0; db < DB; ++db) voffs[db] = v_frag_off<D>(db, lane);
+
   const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
   const int n_tiles = (kv_end + kBC - 1) / kBC;
   const int n_groups = (n_tiles + KSPLIT - 1) / KSPLIT;
+  // Groups [0, g_full) hold no key >= N and, if CAUSAL, no key above the
+  // workgroup's first row: their scores need no mask.
+  const int lim = CAUSAL ? min(N, q0 + 1) : N;
+  const int g_full = lim / (KSPLIT * kBC);
 
   const uint32_t lds0 = lds_addr(smem);
-  auto issue_k = [&](int g, int stage) {
+  auto issue = [&](int x, int base_slot) {   // K(x) (base_slot 0) or V(x) (base_slot RING)
+    const char* src = base_slot == 0 ? Kh : Vh;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int t = g * KSPLIT + slot_of[i];
-      dma_block_or_zero<D, FULL>(Kh, head_bytes, t, t < n_tiles,
-                                 lds0 + stage * GROUP + slot_of[i] * TILE + blk_of[i] * 1024,
-                                 koff[i]);
+      const int t = x * KSPLIT + slot_of[i];
+      const uint32_t at = lds0 + (base_slot + x % RING) * GROUP + slot_of[i] * TILE + blk_of[i] * 1024;
+      dma_block_or_zero<D, FULL>(src, head_bytes, t, t < n_tiles, at,
+                                 base_slot == 0 ? koff[i] : voff[i]);
     }
   };
-  auto issue_v = [&](int g, int stage) {
+  auto k_base = [&](int x) -> const char* { return smem + (x % RING) * GROUP + ks * TILE; };
+  auto v_base = [&](int x) -> const char* { return smem + (RING + x % RING) * GROUP + ks * TILE; };
+  // Per-lane bases of the operand reads from K(x) and V(y).
+  struct Bases {
+    lds_cp k[D / 16];
+    lds_cp v[DB];
+  };
+  auto bases = [&](int x, int y) {
+    Bases r;
+    // Slot bases as scalars (opaque, so no per-lane share of the slot
+    // arithmetic is folded into the lane offsets).
+    uint32_t kt = lds0 + (x % RING) * GROUP + ks * TILE;
+    uint32_t vt = lds0 + (RING + y % RING) * GROUP + ks * TILE;
+    asm("" : "+s"(kt), "+s"(vt));
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int t = g * KSPLIT + slot_of[i];
-      dma_block_or_zero<D, FULL>(Vh, head_bytes, t, t < n_tiles,
-                                 lds0 + (2 + stage) * GROUP + slot_of[i] * TILE + blk_of[i] * 1024,
-                                 voff[i]);
-    }
+    for (int kk = 0; kk < D / 16; ++kk) r.k[kk] = lds_lane_base(kt + koffs[kk]);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) r.v[db] = lds_lane_base(vt + voffs[db]);
+    return r;
   };
 
-  // This wave's tile in group g is g * KSPLIT + ks. A slice whose tile is past
-  // the end (last group of an odd tile count) processes it fully masked
-  // (P = 0), which keeps the pipeline's shape uniform.
-  const int tile_of = ks;   // t = g * KSPLIT + tile_of
-  auto mask_tile = [&](int t, f32x16 (&s)[2]) {
-    if (t >= n_tiles) {
-#pragma unroll
-      for (int b = 0; b < 2; ++b) s[b] = f32x16{} - INFINITY;
-    } else {
-      rb.template mask<2>(t, 0, s);
-    }
+  // Operand of MFMA m of a step. Steps with a PV alternate (even m: QK i =
+  // m/2, odd m: PV i = m/2); the first step has QK only. QK i: block i % 2,
+  // k-step i / 2. PV i: k-step i / DB, d-block i % DB. Consecutive MFMAs on
+  // one accumulator are four (two) MFMAs apart.
+  auto fetch = [&](auto prev, int m, const Bases& bs) -> f16x8 {
+    constexpr bool PREV = decltype(prev)::value;
+    const int i = PREV ? m >> 1 : m;
+    if (!PREV || (m & 1) == 0) return lds_b128(bs.k[i / 2] + (i % 2) * 32 * 2 * D);
+    return v_frag_lds<D>(bs.v[i % DB] + (i / DB) * 16 * 2 * D);
   };
 
-  // Prologue: K(0), K(1) in, S(0) computed.
-  f32x16 s_cur[2];
-  issue_k(0, 0);
-  if (n_groups > 1) issue_k(1, 1);
-  wait_vmem();
+  // Prologue: K(0 .. RING-1) and V(0 .. RING-3) in flight; K(0), K(1) landed.
+#pragma unroll
+  for (int x = 0; x < RING; ++x) issue(x, 0);
+#pragma unroll
+  for (int x = 0; x < RING - 2; ++x) issue(x, RING);
+  wait_vmcnt<(RING - 2) * PER_STEP>();
   __syncthreads();
-  rb.template qk<2>(smem + ks * TILE, 0, s_cur);
-  mask_tile(tile_of, s_cur);
 
-  f16x8 pf[4];   // P of the previous group's tile, packed: the B operands of its PV
-  auto step = [&](auto par, auto has_prev, auto has_next, int g) {
-    constexpr int PAR = decltype(par)::value;          // g & 1
-    constexpr bool PREV = decltype(has_prev)::value;   // g >= 1
-    constexpr bool NEXT = decltype(has_next)::value;   // g + 1 < n_groups
-    if (g + 2 < n_groups) issue_k(g + 2, PAR);         // K(g) was consumed by step g-1
-    issue_v(g, PAR);                                   // V(g-2) was consumed by step g-1
-    const char* k_next = smem + (1 - PAR) * GROUP + ks * TILE;        // K(g+1)
-    const char* v_prev = smem + (2 + (1 - PAR)) * GROUP + ks * TILE;  // V(g-1)
-    f32x16 s_nxt[2];
-    if constexpr (NEXT) rb.template qk<2>(k_next, 0, s_nxt);
-    if constexpr (PREV) rb.template pv<2>(v_prev, 0, pf);
-    rb.template softmax_keep<2>(s_cur, pf);
-    if constexpr (NEXT) {
-      mask_tile((g + 1) * KSPLIT + tile_of, s_nxt);
-      s_cur[0] = s_nxt[0];
-      s_cur[1] = s_nxt[1];
-    }
-    wait_vmem();
-    __syncthreads();
-  };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
+  f32x16 sA[2], sB[2];   // scores of the tile being softmaxed / being computed
+  f16x8 pA[4], pB[4];    // packed P of the tile whose PV is pending / being made
+  f16x8 a[PF];           // operands of the next step's first PF MFMAs
+  rb.template qk<2>(k_base(0), 0, sA);
+  __syncthreads();       // K(0) read by every wave: its slot is refilled next
+  issue(RING, 0);        // step 0's copies: K(RING), V(RING-2)
+  issue(RING - 2, RING);
   using BT = std::true_type;
   using BF = std::false_type;
-  if (n_groups == 1) {
-    step(I0{}, BF{}, BF{}, 0);
-  } else {
-    step(I0{}, BF{}, BT{}, 0);
-    int g = 1;
-    for (; g + 2 < n_groups; g += 2) {
-      step(I1{}, BT{}, BT{}, g);
-      step(I0{}, BT{}, BT{}, g + 1);
-    }
-    if (n_groups - g == 2) {
-      step(I1{}, BT{}, BT{}, g);
-      step(I0{}, BT{}, BF{}, g + 1);
-    } else {
-      step(I1{}, BT{}, BF{}, g);
-    }
+  Bases nb = bases(1, RING - 1);   // bases of the next step (V unused in step 0)
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = fetch(BF{}, i, nb);
+
+  // One step. cur: S(g); nxt: S(g+1) out; pin: P(g-1); pout: P(g) out.
+  auto step = [&](auto prev, auto masked, int g, f32x16 (&cur)[2], f32x16 (&nxt)[2],
+                  const f16x8 (&pin)[4], f16x8 (&pout)[4]) {
+    constexpr bool PREV = decltype(prev)::value;       // g >= 1
+    constexpr bool MASKED = decltype(masked)::value;   // group g may need a mask
+    constexpr int NM = PREV ? 2 * NMM : NMM;
+    constexpr int MID = NM - MID_BACK;
+    // Bases of K(g+1) (zeros past the end: harmless, unused) and V(g-1),
+    // computed by the previous step.
+    const Bases bs = nb;
+    f16x8 op[NM];
+#pragma unroll
+    for (int m = 0; m < PF; ++m) op[m] = a[m];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) nxt[b] = f32x16{};
+    if constexpr (MASKED) rb.template mask_all<2>(g * KSPLIT + ks, 0, cur);
+    const float m_cur = rb.m_run;
+    float acc[2];
+    float ex[16][2];
+    // Softmax slot u: exponentials of value pair u (u < 16), then the fp16
+    // pack and row-sum of pair u-1 (u >= 1), a slot after its exponentials.
+    auto slot = [&](auto ui) {
+      constexpr int u = decltype(ui)::value;
+      if constexpr (u < 16) {
+        constexpr int b = u / 8, r = 2 * (u % 8);
+        ex[u][0] = exp2_hw(fmaf(cur[b][r], c, -m_cur));
+        ex[u][1] = exp2_hw(fmaf(cur[b][r + 1], c, -m_cur));
+      }
+      if constexpr (u >= 1) {
+        constexpr int p = u - 1, b = p / 8, h = (p % 8) / 4, q = p % 4;
+        f16x2 x = cvt2(ex[p][0], ex[p][1]);
+        // Pin the conversion to this chunk (the slow path also writes P, and
+        // the compiler would otherwise sink it below the branch).
+        asm volatile("" : "+v"(x));
+        if constexpr (p < 2) {
+          acc[p] = ex[p][0] + ex[p][1];
+        } else {
+          acc[p & 1] += ex[p][0] + ex[p][1];
+        }
+        pout[2 * b + h][2 * q] = x[0];
+        pout[2 * b + h][2 * q + 1] = x[1];
+      }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NM>([&](auto mi) {
+      constexpr int m = decltype(mi)::value;
+      if constexpr (m + PF < NM) op[m + PF] = fetch(prev, m + PF, bs);
+      if constexpr (m == MID) {
+        // Every LDS read of this step is issued (the barrier waits for them).
+        wait_vmcnt<(RING - 2) * PER_STEP>();
+        __syncthreads();
+        issue(g + 1 + RING, 0);
+        issue(g + RING - 1, RING);
+        nb = bases(g + 2, g);
+#pragma unroll
+        for (int i = 0; i < PF; ++i) a[i] = fetch(BT{}, i, nb);
+      }
+      if constexpr (PREV) {
+        constexpr int i = m >> 1;
+        if constexpr ((m & 1) == 0) {
+          nxt[i % 2] = mfma32(op[m], rb.qf[i / 2], nxt[i % 2]);
+        } else {
+          rb.o[i % DB] = mfma32(op[m], pin[i / DB], rb.o[i % DB]);
+        }
+      } else {
+        nxt[m % 2] = mfma32(op[m], rb.qf[m / 2], nxt[m % 2]);
+      }
+      static_for<m * NSLOT / NM, (m + 1) * NSLOT / NM>(slot);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    float rs = acc[0] + acc[1];
+    // Rare: copies for the merge of O and P go on this edge, not the fast one.
+    if (__builtin_expect(!__all(rs <= kSumLimit), 0)) rs = rb.template rescue<2>(cur, pout);
+    rb.l_run += rs;
+  };
+
+  // Step 0 (no PV yet; always masked: cheap, and covers g_full == 0).
+  // Odd steps then read sB / pA and write sA / pB, even steps the reverse.
+  step(BF{}, BT{}, 0, sA, sB, pB, pA);
+  int g = 1;
+  for (; g + 1 < g_full; g += 2) {
+    step(BT{}, BF{}, g, sB, sA, pA, pB);
+    step(BT{}, BF{}, g + 1, sA, sB, pB, pA);
   }
-  // PV of the last group: its V landed in stage (n_groups-1) & 1 in the last step.
-  rb.template pv<2>(smem + (2 + ((n_groups - 1) & 1)) * GROUP + ks * TILE, 0, pf);
+  if (g < g_full) {
+    step(BT{}, BF{}, g, sB, sA, pA, pB);
+    ++g;
+  }
+  if ((g & 1) == 0 && g < n_groups) {
+    step(BT{}, BT{}, g, sA, sB, pB, pA);
+    ++g;
+  }
+  for (; g + 1 < n_groups; g += 2) {
+    step(BT{}, BT{}, g, sB, sA, pA, pB);
+    step(BT{}, BT{}, g + 1, sA, sB, pB, pA);
+  }
+  if (g < n_groups) step(BT{}, BT{}, g, sB, sA, pA, pB);
+
+  // PV of the last group: V(n_groups-1) landed before the last step's
+  // barrier; its P is in pB if n_groups-1 is odd, else in pA.
+  {
+    const bool odd = ((n_groups - 1) & 1) != 0;
+    f16x8 pl[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pl[j] = odd ? pB[j] : pA[j];
+    rb.template pv<2>(v_base(n_groups - 1), 0, pl);
+  }
+  wait_vmem();   // the last steps' copies (all of empty ranges) have drained
 
   if constexpr (KSPLIT > 1) {
     // Merge the key slices of each row group through LDS (see the split kernel).
     __syncthreads();
-    constexpr int REC = (2 + 16 * RB::DB) * 64;
+    constexpr int REC = (2 + 16 * DB) * 64;
     float* area = reinterpret_cast<float*>(smem + rg * GROUP);
     if (ks > 0) rb.save_to(area + (ks - 1) * REC);
     __syncthreads();
@@ -657,10 +742,252 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   rb.template finish<WRITE_L>(O + head, L + (size_t)bh * N);
 }
 
+// ---------------------------------------------------------------------------
+// Ping-pong kernel: 8 waves. Wave w is row group w % 4 and group w / 4;
+// group 0 owns the even key tiles and group 1 the odd ones, so waves w and
+// w + 4 (one per group) share a SIMD and the same 32 query rows. Time runs
+// in barrier-separated phases, and in every phase one group issues matrix
+// work (its "M" phase: PV of its current tile and QK of its next one) while
+// the other runs the softmax of its current tile on the VALU ("S" phase):
+//
+//   phase      2j                       2j+1
+//   group 0    S(tile 2j)               M(PV tile 2j, QK tile 2j+2)
+//   group 1    M(PV 2j-1, QK 2j+1)      S(tile 2j+1)
+//
+// The two waves of a SIMD then need different pipes at the same time, so
+// the matrix core and the VALU overlap across waves even though the
+// hardware issues oldest-wave-first; two waves of the same phase kind would
+// run nearly one after the other. Each wave holds one score tile and one
+// packed P tile, and each group runs its own copy of the loop (the same
+// number of barriers), so neither is merged between groups.
+//
+// K and V tiles go through rings of RING slots (tile x in slot x % RING).
+// The copies are issued by the waves in their M phase, between their MFMAs
+// (their issue slots are idle while the matrix core runs): in phase 2j
+// group 1 copies K tile 2j+RING-1 and V tile 2j+RING-3, in phase 2j+1 group
+// 0 copies K tile 2j+RING and V tile 2j+RING-2, each into the slot of a tile
+// read in step j-1; both are read RING-2 phases later. A wave waits for its
+// copies at the end of the S phase just before that, so each copy has about
+// RING/2 - 1 steps to land. Tiles past the end are copied with an empty
+// buffer range (zeros).
+// ---------------------------------------------------------------------------
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING>
+__global__ void __launch_bounds__(512)
+fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                 const f16* __restrict__ V, f16* __restrict__ O,
+                 float* __restrict__ L, int N, int num_qb, int total, float c) {
+  static_assert(RING == 4 || RING == 6, "an even ring of four or six tiles");
+  constexpr int TILE = kBC * D * 2;
+  constexpr int BLOCKS = TILE / 1024;          // 1 KiB blocks per tile
+  constexpr int LOADS = BLOCKS / 4;            // blocks per M-phase wave per tile
+  static_assert(2 * RING * TILE <= 160 * 1024, "slots exceed the 160 KiB LDS");
+  using RB = RowBlock<D, CAUSAL, FULL>;
+  constexpr int DB = RB::DB;
+  constexpr int KSTEPS = D / 16;
+  constexpr int NMM = D / 8;                   // MFMAs of one QK (= of one PV)
+  constexpr int PF = 4;                        // operand prefetch distance, in MFMAs
+  constexpr int REC = (2 + 16 * DB) * 64;      // floats per wave record of the merge
+  static_assert(kRowGroups * REC * 4 <= 2 * RING * TILE, "merge area too small");
+  // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
+  __shared__ __attribute__((aligned(1024))) char smem[2 * RING * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: SGPR
+  const int rg = wave & (kRowGroups - 1);
+  const int grp = wave >> 2;
+
+  const int logical = xcd_remap(blockIdx.x, total);
+  const int bh = logical / num_qb;
+  int qb = logical - bh * num_qb;
+  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
+
+  const size_t head = (size_t)bh * N * D;
+  const int head_bytes = N * D * 2;
+  const char* Kh = reinterpret_cast<const char*>(K + head);
+  const char* Vh = reinterpret_cast<const char*>(V + head);
+  const int q0 = qb * kBR;
+
+  RB rb;
+  rb.init(Q + head, head_bytes, lane, q0 + 32 * rg, N, c);
+
+  const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
+  const int n_tiles = (kv_end + kBC - 1) / kBC;
+  const int n_steps = (n_tiles + 1) / 2;       // tiles per group
+
+  const uint32_t lds0 = lds_addr(smem);
+  // This wave's share of a tile copy in its M phase: blocks rg*LOADS .. +LOADS.
+  uint32_t koff[LOADS], voff[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) dma_offsets<D>(rg * LOADS + i, lane, koff[i], voff[i]);
+  auto copy_block = [&](bool is_v, int t, int i) {
+    const uint32_t at = lds0 + ((is_v ? RING : 0) + t % RING) * TILE + (rg * LOADS + i) * 1024;
+    dma_block_or_zero<D, FULL>(is_v ? Vh : Kh, head_bytes, t, t < n_tiles, at, is_v ? voff[i] : koff[i]);
+  };
+
+  // Per-lane offsets of the operand fragments within a tile.
+  int koffs[KSTEPS], voffs[DB];
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) koffs[kk] = k_frag_off<D>(kk, lane);
+#pragma unroll
+  for (int db = 0; db < DB; ++db) voffs[db] = v_frag_off<D>(db, lane);
+
+  // Prologue: every wave copies its share (1/8) of K tiles 0 .. RING-2 and
+  // V tiles 0 .. RING-4 (those read before the first M-phase copies land).
+  {
+    constexpr int PB = BLOCKS / 8;
+    uint32_t ko[PB], vo[PB];
+#pragma unroll
+    for (int i = 0; i < PB; ++i) dma_offsets<D>(wave * PB + i, lane, ko[i], vo[i]);
+#pragma unroll
+    for (int x = 0; x < RING - 1; ++x) {
+#pragma unroll
+      for (int i = 0; i < PB; ++i)
+        dma_block_or_zero<D, FULL>(Kh, head_bytes, x, x < n_tiles,
+                                   lds0 + x * TILE + (wave * PB + i) * 1024, ko[i]);
+    }
+#pragma unroll
+    for (int x = 0; x < RING - 3; ++x) {
+#pragma unroll
+      for (int i = 0; i < PB; ++i)
+        dma_block_or_zero<D, FULL>(Vh, head_bytes, x, x < n_tiles,
+                                   lds0 + (RING + x) * TILE + (wave * PB + i) * 1024, vo[i]);
+    }
+  }
+  wait_vmem();
+  __syncthreads();
+
+  f32x16 s[2];    // scores of this wave's current tile
+  f16x8 p[4];     // its packed P
+
+  using BT = std::true_type;
+  using BF = std::false_type;
+
+  // M phase: PV of tile tv (P in p; skipped without PV) and QK of tile tq
+  // into s, alternating, with the operand reads PF MFMAs ahead; between
+  // them, this wave's share of the copies of K tile ck and V tile cv.
+  auto mphase = [&](auto with_pv, int tq, int tv, int ck, int cv) {
+    constexpr bool PV = decltype(with_pv)::value;
+    constexpr int NM = PV ? 2 * NMM : NMM;
+    constexpr int NC = 2 * LOADS;              // copies of this phase
+    uint32_t kt = lds0 + (tq % RING) * TILE;
+    uint32_t vt = lds0 + (RING + tv % RING) * TILE;
+    asm("" : "+s"(kt), "+s"(vt));
+    lds_cp kl[KSTEPS], vl[DB];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) kl[kk] = lds_lane_base(kt + koffs[kk]);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) vl[db] = lds_lane_base(vt + voffs[db]);
+    // MFMA m: with PV, even m = PV i, odd m = QK i (i = m / 2); else QK m.
+    // QK i: block i % 2, k-step i / 2. PV i: k-step i / DB, d-block i % DB.
+    auto fetch = [&](int m) -> f16x8 {
+      const int i = PV ? m >> 1 : m;
+      if (PV && (m & 1) == 0) return v_frag_lds<D>(vl[i % DB] + (i / DB) * 16 * 2 * D);
+      return lds_b128(kl[i / 2] + (i % 2) * 32 * 2 * D);
+    };
+    f16x8 op[NM];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) s[b] = f32x16{};
+#pragma unroll
+    for (int m = 0; m < PF; ++m) op[m] = fetch(m);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NM>([&](auto mi) {
+      constexpr int m = decltype(mi)::value;
+      if constexpr (m + PF < NM) op[m + PF] = fetch(m + PF);
+      constexpr int i = PV ? m >> 1 : m;
+      if constexpr (PV && (m & 1) == 0) {
+        rb.o[i % DB] = mfma32(op[m], p[i / DB], rb.o[i % DB]);
+      } else {
+        s[i % 2] = mfma32(op[m], rb.qf[i / 2], s[i % 2]);
+      }
+      // Copy c of this phase after MFMA (c + 1) * NM / (NC + 1).
+      static_for<0, NC>([&](auto ci) {
+        constexpr int cc = decltype(ci)::value;
+        if constexpr ((cc + 1) * NM / (NC + 1) == m) copy_block(cc >= LOADS, cc >= LOADS ? cv : ck, cc % LOADS);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // S phase: softmax of tile t (scores in s) into p, the exponentials of a
+  // value pair consumed two pairs later.
+  auto sphase = [&](int t) {
+    rb.template mask<2>(t, 0, s);
+    const float m_cur = rb.m_run;
+    float ex[16][2];
+    float acc[2];
+    auto slot = [&](auto ui) {
+      constexpr int u = decltype(ui)::value;
+      if constexpr (u < 16) {
+        constexpr int b = u / 8, r = 2 * (u % 8);
+        ex[u][0] = exp2_hw(fmaf(s[b][r], c, -m_cur));
+        ex[u][1] = exp2_hw(fmaf(s[b][r + 1], c, -m_cur));
+      }
+      if constexpr (u >= 2) {
+        constexpr int q2 = u - 2, b = q2 / 8, h = (q2 % 8) / 4, q = q2 % 4;
+        const f16x2 x = cvt2(ex[q2][0], ex[q2][1]);
+        if constexpr (q2 < 2) {
+          acc[q2] = ex[q2][0] + ex[q2][1];
+        } else {
+          acc[q2 & 1] += ex[q2][0] + ex[q2][1];
+        }
+        p[2 * b + h][2 * q] = x[0];
+        p[2 * b + h][2 * q + 1] = x[1];
+      }
+    };
+    static_for<0, 18>(slot);
+    float rs = acc[0] + acc[1];
+    if (__builtin_expect(!__all(rs <= kSumLimit), 0)) rs = rb.template rescue<2>(s, p);
+    rb.l_run += rs;
+    // This wave's copies of its M phase RING/2 - 1 phases of its own back;
+    // those of the later M phases stay in flight.
+    wait_vmcnt<(RING / 2 - 2) * 2 * LOADS>();
+  };
+
+  if (grp == 0) {
+    rb.template qk<2>(smem, 0, s);   // tile 0 (slot 0)
+    __syncthreads();                 // slot 0 is refilled in phase 1
+    for (int j = 0; j < n_steps; ++j) {
+      sphase(2 * j);
+      __syncthreads();
+      mphase(BT{}, 2 * j + 2, 2 * j, 2 * j + RING, 2 * j + RING - 2);
+      __syncthreads();
+    }
+    __syncthreads();   // group 1's last PV
+  } else {
+    __syncthreads();
+    for (int j = 0; j < n_steps; ++j) {
+      if (j == 0) {
+        mphase(BF{}, 1, 0, RING - 1, RING - 3);
+      } else {
+        mphase(BT{}, 2 * j + 1, 2 * j - 1, 2 * j + RING - 1, 2 * j + RING - 3);
+      }
+      __syncthreads();
+      sphase(2 * j + 1);
+      __syncthreads();
+    }
+    // Phase 2n: the last PV.
+    rb.template pv<2>(smem + (RING + (2 * n_steps - 1) % RING) * TILE, 0, p);
+    __syncthreads();
+  }
+  wait_vmem();   // copies of the last M phases
+
+  // Merge group 1 into group 0 through LDS (the ring is free: all copies
+  // have landed and every read is done).
+  float* area = reinterpret_cast<float*>(smem) + rg * REC;
+  __syncthreads();
+  if (grp == 1) rb.save_to(area);
+  __syncthreads();
+  if (grp == 1) return;
+  rb.merge_from(area);
+  rb.template finish<WRITE_L>(O + head, L + (size_t)bh * N);
+}
+
 // Kernel variants: 10*k + s = split kernel with KSPLIT k and s LDS stages;
-// 100 + k = pipelined kernel with KSPLIT k.
-constexpr int kPipe1 = 101;
-constexpr int kPipe2 = 102;
+// 100 + 10*r + k = pipelined kernel with KSPLIT k and a ring of r slots;
+// 200 + r = ping-pong kernel with a ring of r tiles.
+constexpr int kPingPong = 204;
+constexpr int pipe_code(int ksplit, int ring) { return 100 + 10 * ring + ksplit; }
 
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
 static void launch_split(const f16* Q, const f16* K, const f16* V, f16* O, float* L, int N,
@@ -669,13 +996,25 @@ static void launch_split(const f16* Q, const f16* K, const f16* V, f16* O, float
                      dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, N, num_qb, total, c);
 }
 
-// Variants whose LDS fits: 2 * STAGES * KSPLIT * (64 * D * 2) <= 160 KiB.
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int RING>
+static void launch_pipe(const f16* Q, const f16* K, const f16* V, f16* O, float* L, int N,
+                        int num_qb, int total, float c, hipStream_t stream) {
+  hipLaunchKernelGGL((fa_fwd_pipe_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, RING>), dim3(total),
+                     dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, N, num_qb, total, c);
+}
+
+// Variants that exist and whose LDS fits in 160 KiB.
 static bool variant_fits(int D, int variant) {
-  if (variant == kPipe1) return true;
-  if (variant == kPipe2) return 4 * 2 * (64 * D * 2) <= 160 * 1024;
+  const int tile = 64 * D * 2;
+  if (variant == kPingPong) return true;
+  if (variant > 100) {
+    const int ks = variant % 10, ring = (variant - 100) / 10;
+    if ((ks != 1 && ks != 2) || ring < 2 || ring > 4) return false;
+    return 2 * ring * ks * tile <= 160 * 1024;
+  }
   const int ks = variant / 10, st = variant % 10;
   if ((ks != 1 && ks != 2 && ks != 4) || st < 2 || st > 4) return false;
-  return 2 * st * ks * (64 * D * 2) <= 160 * 1024;
+  return 2 * st * ks * tile <= 160 * 1024;
 }
 
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL>
@@ -687,14 +1026,17 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
   const f16* V = (const f16*)v;
   f16* Op = (f16*)o;
   switch (variant) {
-    case kPipe1:
-      hipLaunchKernelGGL((fa_fwd_pipe_kernel<D, CAUSAL, WRITE_L, FULL, 1>), dim3(total), dim3(256), 0,
+    case kPingPong:
+      hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4>), dim3(total), dim3(512), 0,
                          stream, Q, K, V, Op, lse, N, num_qb, total, c);
       break;
-    case kPipe2:
-      hipLaunchKernelGGL((fa_fwd_pipe_kernel<D, CAUSAL, WRITE_L, FULL, 2>), dim3(total), dim3(512), 0,
-                         stream, Q, K, V, Op, lse, N, num_qb, total, c);
-      break;
+    case pipe_code(1, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
+    case pipe_code(1, 3): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
+    case pipe_code(1, 4): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
+    case pipe_code(2, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 2, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
+    case pipe_code(2, 3):
+      if constexpr (D == 64) { launch_pipe<D, CAUSAL, WRITE_L, FULL, 2, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break; }
+      return hipErrorInvalidValue;
     case 13: launch_split<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
     case 14: launch_split<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
     case 22: launch_split<D, CAUSAL, WRITE_L, FULL, 2, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
@@ -727,14 +1069,16 @@ static hipError_t dispatch_wl(const void* q, const void* k, const void* v, void*
 }
 
 // Variant choice (measured on MI355X; see bench.py). The environment
-// variable FA_MI355X_FWD_VARIANT ("pipe<k>" or "split<k>s<s>", e.g. split1s4)
+// variable FA_MI355X_FWD_VARIANT ("pipe<k>r<r>" or "split<k>s<s>", e.g.
+// pipe1r3, split1s4)
 // forces one that fits D; it is read once, for measurement and tests.
 static int choose_variant(int64_t D) {
   static const int forced = [] {
     const char* e = getenv("FA_MI355X_FWD_VARIANT");
     if (!e) return -1;
     int ks = 0, st = 0;
-    if (sscanf(e, "pipe%d", &ks) == 1) return 100 + ks;
+    if (strcmp(e, "pingpong") == 0) return kPingPong;
+    if (sscanf(e, "pipe%dr%d", &ks, &st) == 2) return pipe_code(ks, st);
     if (sscanf(e, "split%ds%d", &ks, &st) == 2) return 10 * ks + st;
     return -1;
   }();
@@ -747,19 +1091,21 @@ static int choose_variant(int64_t D) {
 
 }  // namespace fa
 
-extern "C" int fa_fwd_f16(const void* q, const void* k, const void* v, void* o,
-                          float* lse, int64_t B, int64_t H, int64_t N, int64_t D,
-                          int causal, void* stream) {
-  using namespace fa;
+namespace fa {
+// The forward with an explicit kernel variant (0: the default choice).
+static int fwd_with_variant(const void* q, const void* k, const void* v, void* o, float* lse,
+                            int64_t B, int64_t H, int64_t N, int64_t D, int causal, int variant,
+                            void* stream) {
   int st = fa_validate_fwd(q, k, v, o, B, H, N, D);
   if (st != FA_OK) return st;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
+  if (variant == 0) variant = choose_variant(D);
+  if (!variant_fits((int)D, variant)) return FA_ERR_HEAD_DIM;
   const int num_qb = (int)((N + kBR - 1) / kBR);
   const int total = (int)(B * H * num_qb);
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   const bool full = (N % kBR) == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int variant = choose_variant(D);
   hipError_t e;
   if (D == 64) {
     e = causal ? dispatch_wl<64, true>(q, k, v, o, lse, (int)N, num_qb, total, c, full, variant, s)
@@ -769,4 +1115,35 @@ extern "C" int fa_fwd_f16(const void* q, const void* k, const void* v, void* o,
                : dispatch_wl<128, false>(q, k, v, o, lse, (int)N, num_qb, total, c, full, variant, s);
   }
   return e == hipSuccess ? FA_OK : -(int)e;
+}
+}  // namespace fa
+
+extern "C" int fa_fwd_f16(const void* q, const void* k, const void* v, void* o,
+                          float* lse, int64_t B, int64_t H, int64_t N, int64_t D,
+                          int causal, void* stream) {
+  return fa::fwd_with_variant(q, k, v, o, lse, B, H, N, D, causal, 0, stream);
+}
+
+extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o,
+                                    float* lse, int64_t B, int64_t H, int64_t N, int64_t D,
+                                    int causal, int variant, void* stream) {
+  if (variant <= 0) return FA_ERR_HEAD_DIM;
+  return fa::fwd_with_variant(q, k, v, o, lse, B, H, N, D, causal, variant, stream);
+}
+
+extern "C" int fa_probe_default_variant(int64_t D) {
+  if (D != 64 && D != 128) return 0;
+  return fa::choose_variant(D);
+}
+
+extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D) {
+  static const int all[] = {12, 13, 14, 22, 23, 24, 42, 112, 113, 114, 122, 123, 204};
+  int n = 0;
+  for (int v : all) {
+    if (fa::variant_fits((int)D, v)) {
+      if (out != nullptr && n < max_out) out[n] = v;
+      ++n;
+    }
+  }
+  return n;
 }

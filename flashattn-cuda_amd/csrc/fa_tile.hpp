@@ -128,12 +128,48 @@ __device__ __forceinline__ int k_off(int r, int c) { return r * (2 * D) + k_slot
 template <int D>
 __device__ __forceinline__ int v_off(int r, int c) { return r * (2 * D) + v_slot<D>(r, c) * 16; }
 
+// LDS pointers for the pipelined kernel's operand reads: arithmetic on them
+// stays in the 32-bit LDS address space, so constant offsets fold into the
+// DS instructions' offset field.
+typedef const __attribute__((address_space(3))) char* lds_cp;
+
+// A lane's base address in LDS, opaque to the optimiser: every read of the
+// step is then this base plus a constant, instead of a separately hoisted
+// loop-invariant offset plus the step's slot base per read.
+__device__ __forceinline__ lds_cp lds_lane_base(uint32_t a) {
+  asm("" : "+v"(a));
+  return (lds_cp)(size_t)a;
+}
+
+__device__ __forceinline__ f16x8 lds_b128(lds_cp p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) f16x8*>(p);
+}
+
+__device__ __forceinline__ f16x4 lds_tr16(lds_cp p) {
+  typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+  fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)(p));
+  return __builtin_bit_cast(f16x4, v);
+}
+
+// V fragment (see load_v_frag) whose k-step-0 address is p.
+template <int D>
+__device__ __forceinline__ f16x8 v_frag_lds(lds_cp p) {
+  f16x4 lo = lds_tr16(p);
+  f16x4 up = lds_tr16(p + 8 * 2 * D);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+}
+
 // A operand of S^T = K Q^T for key block kb (32 keys) and k-step kk (16 of D).
+// The K swizzle depends on the row only modulo 16, so block kb is the block-0
+// fragment shifted by 32 rows: k_frag_off(kk, lane) + 32 * kb * 2D.
+template <int D>
+__device__ __forceinline__ int k_frag_off(int kk, int lane) {
+  return k_off<D>(lane & 31, 2 * kk + (lane >> 5));
+}
+
 template <int D>
 __device__ __forceinline__ f16x8 load_k_frag(const char* ks, int kb, int kk, int lane) {
-  const int r = 32 * kb + (lane & 31);
-  const int c = 2 * kk + (lane >> 5);
-  return *reinterpret_cast<const f16x8*>(ks + k_off<D>(r, c));
+  return *reinterpret_cast<const f16x8*>(ks + 32 * kb * 2 * D + k_frag_off<D>(kk, lane));
 }
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane s supplies the
@@ -150,19 +186,29 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const char* p) {
 // A operand of O^T = V^T P^T for PV k-step j (16 keys of the 64-key tile) and
 // d-block db (32 of D). Slot i of lane l must hold V[key(j, i, l)][32*db + l%32]
 // with key(j, i, l) = 16*j + 8*(i/4) + 4*(l/32) + i%4, the key order of the
-// S^T accumulator registers (see pack_p).
+// S^T accumulator registers (see pack_p). Lane l reads rows r0 = 4*(l/32) +
+// (l%16)/4 (+16 j) and r0 + 8; the V swizzle depends on the row only modulo
+// 4, so k-step j and the upper 4 keys are constant row shifts of
+// v_frag_off(db, lane).
+template <int D>
+__device__ __forceinline__ int v_frag_off(int db, int lane) {
+  const int s = lane & 15;
+  const int d = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  const int r0 = 4 * (lane >> 5) + (s >> 2);
+  return v_off<D>(r0, d >> 3) + 8 * ((d >> 2) & 1);
+}
+
+// The fragment whose k-step j = 0 row-0 address is p (= tile + v_frag_off).
+template <int D>
+__device__ __forceinline__ f16x8 v_frag_at(const char* p) {
+  f16x4 lo = lds_read_tr16(p);
+  f16x4 up = lds_read_tr16(p + 8 * 2 * D);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+}
+
 template <int D>
 __device__ __forceinline__ f16x8 load_v_frag(const char* vs, int j, int db, int lane) {
-  const int s = lane & 15;
-  const int hi = lane >> 5;
-  const int d = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
-  const int c = d >> 3;
-  const int half = (d >> 2) & 1;
-  const int r0 = 16 * j + 4 * hi + (s >> 2);
-  const int r1 = r0 + 8;
-  f16x4 lo = lds_read_tr16(vs + v_off<D>(r0, c) + 8 * half);
-  f16x4 up = lds_read_tr16(vs + v_off<D>(r1, c) + 8 * half);
-  return f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+  return v_frag_at<D>(vs + 16 * j * 2 * D + v_frag_off<D>(db, lane));
 }
 
 // Key index (within a 64-key tile) held by register r of key block kb in lane l.

@@ -30,7 +30,8 @@ void check_status(int st, const char* what) {
 }
 
 std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Tensor K,
-                                                     torch::Tensor V, bool want_L, bool causal) {
+                                                     torch::Tensor V, bool want_L, bool causal,
+                                                     int variant = 0) {
   TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Q/K/V must be CUDA tensors");
   TORCH_CHECK(Q.dim() == 4, "Q must be 4D [B, H, N, D]");
   const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
@@ -55,8 +56,12 @@ std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Ten
     L = torch::empty({BH, N}, Qh.options().dtype(torch::kFloat));
     L_ptr = L.data_ptr<float>();
   }
-  const int st = fa_fwd_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H,
-                            N, D, causal ? 1 : 0, current_stream(Qh));
+  const int st =
+      variant == 0
+          ? fa_fwd_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H, N, D,
+                       causal ? 1 : 0, current_stream(Qh))
+          : fa_probe_fwd_variant(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr,
+                                 B, H, N, D, causal ? 1 : 0, variant, current_stream(Qh));
   check_status(st, "fa_fwd_f16");
   return {O.reshape({B, H, N, D}), want_L ? L.reshape({B, H, N}) : torch::Tensor()};
 }
@@ -68,6 +73,21 @@ std::vector<torch::Tensor> forward(torch::Tensor Q, torch::Tensor K, torch::Tens
 
 torch::Tensor forward_only(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal) {
   return forward_impl(Q, K, V, /*want_L=*/false, causal).first;
+}
+
+// Test support: the forward through one explicit kernel variant.
+std::vector<torch::Tensor> probe_fwd_variant(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                             bool causal, int64_t variant, bool want_L) {
+  TORCH_CHECK(variant > 0, "variant must be > 0");
+  auto r = forward_impl(Q, K, V, want_L, causal, (int)variant);
+  if (want_L) return {r.first, r.second};
+  return {r.first};
+}
+
+std::vector<int64_t> probe_fwd_variants(int64_t D) {
+  int buf[64];
+  const int n = fa_probe_fwd_variants(buf, 64, D);
+  return std::vector<int64_t>(buf, buf + (n < 64 ? n : 64));
 }
 
 struct DecodeArgs {
@@ -250,5 +270,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("probe_permlane", &probe_permlane);
   m.def("probe_frags", &probe_frags);
   m.def("probe_chain", &probe_chain);
+  m.def("probe_fwd_variant", &probe_fwd_variant, py::arg("Q"), py::arg("K"), py::arg("V"),
+        py::arg("causal") = false, py::arg("variant") = 12, py::arg("want_L") = true);
+  m.def("probe_fwd_variants", &probe_fwd_variants);
+  m.def("probe_default_variant", [](int64_t D) { return fa_probe_default_variant(D); });
   m.def("abi_version", &fa_abi_version);
 }

@@ -43,6 +43,22 @@ int fa_probe_frags(const void* tile, void* kout, void* vout, int64_t D, void* st
 int fa_probe_chain(const void* q, const void* k, const void* v, float* o, int64_t D,
                    void* stream);
 
+/* fa_fwd_f16 with an explicit kernel variant (the codes fa_probe_fwd_variants
+ * lists for D), so the tests can check every variant in one process. Returns
+ * FA_ERR_HEAD_DIM for a variant that does not exist for D. */
+int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o, float* lse,
+                         int64_t B, int64_t H, int64_t N, int64_t D, int causal, int variant,
+                         void* stream);
+
+/* The variant fa_fwd_f16 runs for head dimension D (0 for another D):
+ * 10*k + s = split kernel (k key slices, s LDS stages), 100 + 10*r + k =
+ * pipelined kernel (k key slices, ring of r slots), 204 = ping-pong kernel. */
+int fa_probe_default_variant(int64_t D);
+
+/* Writes up to max_out variant codes that exist for head dimension D into out
+ * (may be NULL) and returns how many there are. */
+int fa_probe_fwd_variants(int* out, int max_out, int64_t D);
+
 #ifdef __cplusplus
 }
 #endif

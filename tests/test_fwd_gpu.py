@@ -241,3 +241,26 @@ def test_binding_errors_on_gpu(fa, dev):
         fa.forward(x, torch.zeros(1, 1, 9, 64, device=dev), x)
     with pytest.raises(RuntimeError, match="4D"):
         fa.forward(x[0], x[0], x[0])
+
+
+# Every kernel variant of the forward (the default picks one per D; the others
+# stay selectable for measurement), against the oracle on ragged, causal and
+# aligned shapes, through the same C ABI with an explicit variant code.
+VARIANT_CASES = [(1, 1, 64, False), (1, 2, 200, False), (1, 2, 300, True), (2, 3, 1000, True),
+                 (1, 2, 1024, False), (1, 1, 4095, True)]
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_every_kernel_variant(fa, dev, D):
+    variants = list(fa.probe.probe_fwd_variants(D))
+    assert len(variants) >= 4, variants
+    for B, H, N, causal in VARIANT_CASES:
+        Q, K, V = make_fwd_inputs(B, H, N, D, seed=N + D, amp=1.0)
+        tq, tk, tv = _to_dev(dev, Q, K, V)
+        Or, Lr = naive_attention(half_cast(Q), half_cast(K), half_cast(V), causal=causal)
+        for v in variants:
+            O, L = fa.probe.probe_fwd_variant(tq, tk, tv, causal, v, True)
+            (O2,) = fa.probe.probe_fwd_variant(tq, tk, tv, causal, v, False)
+            torch.cuda.synchronize()
+            assert torch.equal(O, O2), f"variant {v}: O-only differs"
+            _check(O, L, Or, Lr, 1.0, tag=f"variant {v} B{B} H{H} N{N} D{D} causal={causal}")
