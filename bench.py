@@ -1,7 +1,7 @@
 """Benchmark: FlashAttention forward TFLOP/s (and % of dense FP16 MFMA peak) at
 B=1 H=8 N=4096 D=64 on one MI355X, plus the split-KV paged decode in GB/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|decode|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|copy]
 
 A step is one ``forward(Q, K, V)`` call (O fp16 + L fp32) of the headline
 configuration (N=4096) on inputs resident in HBM.
@@ -120,6 +120,28 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
     }
 
 
+def bench_backward(fa, torch, dev, reps=5, iters=20):
+    """Backward (dQ, dK, dV from O, L, dO) at the headline shape and at config 3.
+
+    TFLOP/s counts the usual 2.5x the forward's products (S, dP, dV, dK, dQ:
+    5 of 2 N^2 D each per head); the three-kernel design recomputes S and dP in
+    the dQ kernel, so it executes 7.
+    """
+    res = {}
+    for (B, H, N, D, causal) in ((1, 8, 4096, 64, False), (1, 8, 4096, 64, True),
+                                 (4, 16, 4096, 128, True)):
+        q, k, v = make_fwd(torch, dev, B, H, N, D, seed=N + D)
+        g = torch.randn_like(q)
+        o, lse = fa.forward(q, k, v, causal=causal)
+        ms = median_of(lambda: fa.backward(q, k, v, o, g, lse, causal=causal), reps, 3, iters, torch)
+        f = 2.5 * fwd_flops(B, H, N, D, causal=causal)
+        res[f"B{B}H{H}N{N}D{D}{'_causal' if causal else ''}"] = {
+            "ms": round(ms, 4), "TFLOPs": round(f / ms / 1e9, 1),
+            "pct_peak": round(100 * f / ms / 1e9 / PEAK_FP16_TFLOPS, 2)}
+        del q, k, v, g, o, lse
+    return res
+
+
 def cpu_baseline(budget_s=20.0):
     """Numpy oracle on the headline workload, bounded: whole heads until ~budget_s."""
     import numpy as np
@@ -183,7 +205,7 @@ def main():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "fwd", "decode", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "copy"], default="all")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -204,6 +226,9 @@ def main():
         return
     if args.only == "decode":
         print(json.dumps({"decode": bench_decode(fa, torch, dev)}))
+        return
+    if args.only == "bwd":
+        print(json.dumps({"backward": bench_backward(fa, torch, dev)}))
         return
 
     B, H, N, D = 1, 8, 4096, 64
@@ -275,6 +300,7 @@ def main():
         del q, k, v
         out["extra"] = extra
         out["decode"] = bench_decode(fa, torch, dev)
+        out["backward"] = bench_backward(fa, torch, dev)
         out["copy_calibration"] = copy_calibration(torch, dev)
     if not args.no_cpu and args.only == "all":
         out["cpu_baseline"] = cpu_baseline(args.cpu_budget)

@@ -6,7 +6,12 @@ Drop-in for the reference's torch-extension module
     O, L = forward(Q, K, V)           # O fp16 [B,H,N,D], L fp32 [B,H,N]
     O = forward_only(Q, K, V)         # bitwise the same O, no L
 
-Both accept ``causal=True`` and D in {64, 128}. New entry points:
+Both accept ``causal=True`` and D in {64, 128}. The backward of the
+reference's first module (cuda/flash_attn_kernel.cu:417-503):
+
+    dQ, dK, dV = backward(Q, K, V, O, dO, L)   # fp32 [B,H,N,D]
+
+New entry points:
 
     O, L = decode_paged(q, k_pool, v_pool, page_table, ctx_lens, num_splits=16)
     part_o, part_lse = decode_partials(...);  O, L = lse_combine(part_o, part_lse)
@@ -54,6 +59,14 @@ def forward(Q, K, V, causal: bool = False):
 def forward_only(Q, K, V, causal: bool = False):
     """O only; bitwise equal to forward(...)[0]."""
     return _C.forward_only(Q, K, V, causal)
+
+
+def backward(Q, K, V, O, dO, L, causal: bool = False):
+    """[dQ, dK, dV] (fp32 [B,H,N,D]) of sum(O * dO), from forward()'s O and L.
+
+    The reference's backward(Q, K, V, O, dO, L) (cuda/flash_attn_kernel.cu:417-503).
+    """
+    return _C.backward(Q, K, V, O, dO, L, causal)
 
 
 def decode_paged(q, k_pool, v_pool, page_table, ctx_lens, num_splits: int = 16):

@@ -1,0 +1,450 @@
+// fa_bwd.hip — FlashAttention backward for gfx950 (MI355X): dQ, dK, dV from
+// Q, K, V, O, dO and the forward's logsumexp L.
+//
+// The reference's backward (cuda/flash_attn_kernel.cu:417-503, fp32 math, one
+// thread per row) runs three kernels: D_i = rowsum(dO * O) (:173-191), dQ
+// (:193-...) and dK/dV, each recomputing P = exp(S - L) from the saved L. This
+// file keeps that decomposition — it needs no atomics and no O(N^2) storage —
+// and builds each kernel on v_mfma_f32_32x32x16_f16 with fp32 accumulation:
+//
+//   fa_bwd_di_kernel    D_i = sum_d dO[i][d] * O[i][d]                 (fp32)
+//   fa_bwd_dkdv_kernel  a workgroup owns 128 keys (32 per wave, K and V as
+//                       register operands) and streams 64-query tiles of Q
+//                       and dO (plus L, D_i) through a double-buffered LDS
+//                       ring: S = Q K^T, dP = dO V^T, P = exp2(S c - L log2e),
+//                       dS = P (dP - D_i), dV^T += dO^T P, dK^T += Q^T dS
+//   fa_bwd_dq_kernel    a workgroup owns 128 queries (32 per wave, Q and dO
+//                       as register operands) and streams 64-key tiles of K
+//                       and V: S^T = K Q^T, dP^T = V dO^T, dS^T as above,
+//                       dQ^T += K^T dS^T
+//
+// P and dS are packed to fp16 straight from the score accumulators as the B
+// operands of the gradient products (the reduction index is permuted the same
+// way in both operands, as in the forward). Tiles read both as rows (b128)
+// and transposed (ds_read_b64_tr_b16) are stored in LDS twice, once per
+// swizzle, so both reads stay bank-conflict free.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "fa_mi355x.h"
+#include "fa_tile.hpp"
+
+namespace fa {
+namespace bwd {
+
+constexpr int kBQ = 64;     // rows of a streamed tile
+constexpr int kBlk = 128;   // rows owned by a workgroup (32 per wave)
+
+// Workgroup g of `total` runs logical block xcd-contiguously (see the forward).
+__device__ __forceinline__ int xcd_remap(int g, int total) {
+  const int q = total >> 3, r = total & 7;
+  const int xcd = g & 7, slot = g >> 3;
+  return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
+// Per-lane source offsets of 1 KiB block b of a 64-row tile, for the K-style
+// (row reads) and V-style (transposed reads) LDS swizzles.
+template <int D>
+__device__ __forceinline__ void block_offsets(int b, int lane, uint32_t& koff, uint32_t& voff) {
+  const int o = b * 1024 + 16 * lane;
+  const int r = o / (2 * D);
+  const int slot = (o % (2 * D)) / 16;
+  koff = (uint32_t)(r * 2 * D + (slot ^ k_swz<D>(r)) * 16);
+  voff = (uint32_t)(r * 2 * D + (slot ^ v_swz<D>(r)) * 16);
+}
+
+// A pointer the caller knows to be the same in every lane, moved to SGPRs
+// (buffer resources must be scalar; selects between head pointers otherwise
+// leave the compiler unsure of that).
+template <typename T>
+__device__ __forceinline__ const T* wave_uniform(const T* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Copy 1 KiB block `blk` of 64-row tile t of a head (bytes head_bytes; rows
+// past the end arrive as zeros) into LDS at dst, with per-lane offset off.
+template <int D>
+__device__ __forceinline__ void copy_block(const char* head, int head_bytes, int t, uint32_t dst,
+                                           uint32_t off) {
+  constexpr int TILE = kBQ * D * 2;
+  const int done = t * TILE;
+  const int bytes = max(0, min(TILE, head_bytes - done));
+  dma16(make_rsrc(wave_uniform(head + (bytes > 0 ? done : 0)),
+                  __builtin_amdgcn_readfirstlane(bytes)), dst, off);
+}
+
+// 64 floats of a row vector (L or D_i) starting at row t*64 into 256 bytes of
+// LDS at dst, one per lane (rows >= n arrive as zeros). Dword copies: a head's
+// row vector starts at bh*N floats, only 4-byte aligned.
+__device__ __forceinline__ void copy_rowvec(const float* base, int n, int t, uint32_t dst,
+                                            int lane) {
+  const int done = t * kBQ;
+  const int bytes = max(0, min(kBQ, n - done)) * 4;
+  dma4(make_rsrc(wave_uniform(base + (bytes > 0 ? done : 0)),
+                 __builtin_amdgcn_readfirstlane(bytes)), dst, (uint32_t)(4 * lane));
+}
+
+// B operand (16 x 32) of a product over D from 32 rows of a [N][D] fp16 head:
+// lane l holds row (row0 + l%32), columns 16 kk + 8 (l/32) .. +7 (zeros for
+// rows >= n via the buffer range).
+template <int D>
+__device__ __forceinline__ void load_row_operand(const f16* head, int n, int row0, int lane,
+                                                 f16x8 (&out)[D / 16]) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(head, n * D * 2);
+  const int row = row0 + (lane & 31);
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(
+        r, (uint32_t)(row * D + 16 * kk + 8 * (lane >> 5)) * 2, 0, 0);
+    out[kk] = __builtin_bit_cast(f16x8, x);
+  }
+}
+
+// Store a C-layout accumulator pair-block acc[DB] (rows = 32 d of each block,
+// columns = 32 rows of the output) as fp32 rows out[row][d], scaled.
+template <int D>
+__device__ __forceinline__ void store_transposed(float* out, int n, int row0, int lane,
+                                                 const f32x16 (&acc)[D / 32], float scale) {
+  const int row = row0 + (lane & 31);
+  if (row >= n) return;
+  float* dst = out + (size_t)row * D + 4 * (lane >> 5);
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 v = {acc[db][4 * g] * scale, acc[db][4 * g + 1] * scale, acc[db][4 * g + 2] * scale,
+                 acc[db][4 * g + 3] * scale};
+      *reinterpret_cast<f32x4*>(dst + 32 * db + 8 * g) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// D_i = sum_d dO[i][d] * O[i][d]; 8 lanes per row, one 16-byte chunk each per
+// step (coalesced 128-byte runs), reduced with DPP-free xor shuffles.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(256)
+fa_bwd_di_kernel(const f16* __restrict__ O, const f16* __restrict__ dO, float* __restrict__ Di,
+                 int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int part = threadIdx.x & 7;
+  float acc = 0.f;
+  if (row < rows) {
+    const f16x8* o = reinterpret_cast<const f16x8*>(O + row * D);
+    const f16x8* g = reinterpret_cast<const f16x8*>(dO + row * D);
+#pragma unroll
+    for (int i = part; i < D / 8; i += 8) {
+      const f16x8 a = o[i], b = g[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)b[e], acc);
+    }
+  }
+  acc += __shfl_xor(acc, 1, 8);
+  acc += __shfl_xor(acc, 2, 8);
+  acc += __shfl_xor(acc, 4, 8);
+  if (row < rows && part == 0) Di[row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV. Workgroup = 4 waves = 128 keys of one (b, h); wave w owns keys
+// k0 + 32 w .. +31. Query tiles of 64 rows stream through 2 LDS stages; each
+// stage holds Q and dO twice (row swizzle, transposed swizzle) and 64 floats
+// each of L and D_i.
+// ---------------------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(256)
+fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                   const f16* __restrict__ V, const f16* __restrict__ dO,
+                   const float* __restrict__ L, const float* __restrict__ Di,
+                   float* __restrict__ dK, float* __restrict__ dV, int N, int num_kb, int total,
+                   float c, float scale) {
+  constexpr int TILE = kBQ * D * 2;
+  constexpr int BLOCKS = TILE / 1024;
+  constexpr int KSTEPS = D / 16, DB = D / 32;
+  constexpr int STAGE = 4 * TILE + 2048;       // Qk | Qv | dOk | dOv | L | D_i
+  constexpr int LOADS = 4 * BLOCKS / 4;        // tile blocks per wave per stage
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hi = lane >> 5;
+  const int logical = xcd_remap(blockIdx.x, total);
+  const int bh = logical / num_kb;
+  const int kb = logical - bh * num_kb;
+  const int k0 = kb * kBlk;
+  const int key = k0 + 32 * wave + (lane & 31);
+
+  const size_t head = (size_t)bh * N * D;
+  const int head_bytes = N * D * 2;
+  const char* Qh = reinterpret_cast<const char*>(Q + head);
+  const char* Gh = reinterpret_cast<const char*>(dO + head);
+  const float* Lh = L + (size_t)bh * N;
+  const float* Dh = Di + (size_t)bh * N;
+
+  f16x8 kf[KSTEPS], vf[KSTEPS];   // B operands: K^T and V^T of this wave's keys
+  load_row_operand<D>(K + head, N, k0 + 32 * wave, lane, kf);
+  load_row_operand<D>(V + head, N, k0 + 32 * wave, lane, vf);
+  f32x16 dv[DB], dk[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dv[db] = f32x16{};
+    dk[db] = f32x16{};
+  }
+
+  // Block i of this wave's share of a stage: part (i*4 + wave) / BLOCKS of
+  // {Qk, Qv, dOk, dOv}, block (i*4 + wave) % BLOCKS of that tile.
+  uint32_t off[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int b = i * 4 + wave;
+    uint32_t ko, vo;
+    block_offsets<D>(b % BLOCKS, lane, ko, vo);
+    off[i] = ((b / BLOCKS) & 1) ? vo : ko;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int t, int st) {
+    const uint32_t base = lds0 + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int b = i * 4 + wave;
+      const int part = b / BLOCKS;
+      copy_block<D>(part < 2 ? Qh : Gh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
+                    off[i]);
+    }
+    if (wave == 0) copy_rowvec(Lh, N, t, base + 4 * TILE, lane);
+    if (wave == 1) copy_rowvec(Dh, N, t, base + 4 * TILE + 1024, lane);
+  };
+
+  const int n_qt = (N + kBQ - 1) / kBQ;
+  const int t0 = CAUSAL ? k0 / kBQ : 0;   // earlier query tiles see none of these keys
+  if (t0 < n_qt) {
+    issue(t0, 0);
+    wait_vmem();
+    __syncthreads();
+  }
+  for (int t = t0; t < n_qt; ++t) {
+    const int st = (t - t0) & 1;
+    if (t + 1 < n_qt) issue(t + 1, st ^ 1);
+    const char* sb = smem + st * STAGE;
+    const char* qk = sb;
+    const char* qv = sb + TILE;
+    const char* gk = sb + 2 * TILE;
+    const char* gv = sb + 3 * TILE;
+    const float* ls = reinterpret_cast<const float*>(sb + 4 * TILE);
+    const float* ds = reinterpret_cast<const float*>(sb + 4 * TILE + 1024);
+    const int qt0 = t * kBQ;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      // S and dP for 32 queries x this wave's 32 keys; C layout: register r
+      // holds query qt0 + 32 qb + 8 (r/4) + 4 hi + r%4, lane l key l%32.
+      f32x16 s = {}, dp = {};
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        s = mfma32(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
+        dp = mfma32(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
+      }
+      f32x16 p, g;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int qo = 32 * qb + 8 * r4 + 4 * hi;
+        const f32x4 lq = *reinterpret_cast<const f32x4*>(ls + qo);
+        const f32x4 dq = *reinterpret_cast<const f32x4*>(ds + qo);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          const int q = qt0 + qo + e;
+          float pv = exp2_hw(fmaf(s[r], c, -lq[e] * kLog2e));
+          const bool dead = (q >= N) || (CAUSAL && key > q);
+          pv = dead ? 0.f : pv;
+          p[r] = pv;
+          g[r] = pv * (dp[r] - dq[e]);
+        }
+      }
+      // dV^T += dO^T P and dK^T += Q^T dS over the two 16-query k-steps.
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * qb + h;
+        const f16x8 pb = pack_p(p, h);
+        const f16x8 gb = pack_p(g, h);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          dv[db] = mfma32(load_v_frag<D>(gv, j, db, lane), pb, dv[db]);
+          dk[db] = mfma32(load_v_frag<D>(qv, j, db, lane), gb, dk[db]);
+        }
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+  store_transposed<D>(dV + head, N, k0 + 32 * wave, lane, dv, 1.f);
+  store_transposed<D>(dK + head, N, k0 + 32 * wave, lane, dk, scale);
+}
+
+// ---------------------------------------------------------------------------
+// dQ. Workgroup = 4 waves = 128 queries of one (b, h); wave w owns queries
+// q0 + 32 w .. +31 (Q^T and dO^T as register B operands, L and D_i as lane
+// constants). Key tiles of 64 rows stream through 2 LDS stages, each holding
+// K twice (row swizzle, transposed swizzle) and V once (row swizzle).
+// ---------------------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(256)
+fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                 const f16* __restrict__ V, const f16* __restrict__ dO,
+                 const float* __restrict__ L, const float* __restrict__ Di,
+                 float* __restrict__ dQ, int N, int num_qb, int total, float c, float scale) {
+  constexpr int TILE = kBQ * D * 2;
+  constexpr int BLOCKS = TILE / 1024;
+  constexpr int KSTEPS = D / 16, DB = D / 32;
+  constexpr int STAGE = 3 * TILE;              // Kk | Kv | Vk
+  constexpr int NBLK = 3 * BLOCKS;
+  constexpr int LOADS = (NBLK + 3) / 4;        // tile blocks per wave per stage (some idle)
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hi = lane >> 5;
+  const int logical = xcd_remap(blockIdx.x, total);
+  const int bh = logical / num_qb;
+  int qb = logical - bh * num_qb;
+  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows first
+  const int q0 = qb * kBlk;
+  const int query = q0 + 32 * wave + (lane & 31);
+
+  const size_t head = (size_t)bh * N * D;
+  const int head_bytes = N * D * 2;
+  const char* Kh = reinterpret_cast<const char*>(K + head);
+  const char* Vh = reinterpret_cast<const char*>(V + head);
+
+  f16x8 qf[KSTEPS], gf[KSTEPS];   // B operands: Q^T and dO^T of this wave's queries
+  load_row_operand<D>(Q + head, N, q0 + 32 * wave, lane, qf);
+  load_row_operand<D>(dO + head, N, q0 + 32 * wave, lane, gf);
+  const bool row_ok = query < N;
+  const float lq = row_ok ? L[(size_t)bh * N + query] * kLog2e : 0.f;
+  const float dq_i = row_ok ? Di[(size_t)bh * N + query] : 0.f;
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+
+  uint32_t off[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int b = i * 4 + wave;
+    uint32_t ko, vo;
+    block_offsets<D>(b % BLOCKS, lane, ko, vo);
+    off[i] = ((b / BLOCKS) == 1) ? vo : ko;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int t, int st) {
+    const uint32_t base = lds0 + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int b = i * 4 + wave;
+      if (b < NBLK) {   // wave-uniform
+        const int part = b / BLOCKS;
+        copy_block<D>(part < 2 ? Kh : Vh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
+                      off[i]);
+      }
+    }
+  };
+
+  const int kv_end = CAUSAL ? min(N, q0 + kBlk) : N;
+  const int n_kt = (kv_end + kBQ - 1) / kBQ;
+  issue(0, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int t = 0; t < n_kt; ++t) {
+    const int st = t & 1;
+    if (t + 1 < n_kt) issue(t + 1, st ^ 1);
+    const char* kk_t = smem + st * STAGE;
+    const char* kv_t = kk_t + TILE;
+    const char* vk_t = kk_t + 2 * TILE;
+    const int kt0 = t * kBQ;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      // S^T and dP^T for 32 keys x this wave's 32 queries; register r holds
+      // key kt0 + 32 half + 8 (r/4) + 4 hi + r%4, lane l query l%32.
+      f32x16 s = {}, dp = {};
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        s = mfma32(load_k_frag<D>(kk_t, half, kk, lane), qf[kk], s);
+        dp = mfma32(load_k_frag<D>(vk_t, half, kk, lane), gf[kk], dp);
+      }
+      f32x16 g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kidx = kt0 + 32 * half + 8 * (r >> 2) + 4 * hi + (r & 3);
+        float pv = exp2_hw(fmaf(s[r], c, -lq));
+        const bool dead = (kidx >= N) || (CAUSAL && kidx > query) || !row_ok;
+        pv = dead ? 0.f : pv;
+        g[r] = pv * (dp[r] - dq_i);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * half + h;
+        const f16x8 gb = pack_p(g, h);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db] = mfma32(load_v_frag<D>(kv_t, j, db, lane), gb, acc[db]);
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+  store_transposed<D>(dQ + head, N, q0 + 32 * wave, lane, acc, scale);
+}
+
+template <int D, bool CAUSAL>
+static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
+                             const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                             float* di, int64_t BH, int N, hipStream_t s) {
+  const float scale = (float)(1.0 / sqrt((double)D));
+  const float c = scale * kLog2e;
+  const f16* Q = (const f16*)q;
+  const f16* K = (const f16*)k;
+  const f16* V = (const f16*)v;
+  const f16* O = (const f16*)o;
+  const f16* G = (const f16*)dout;
+  const int64_t rows = BH * N;
+  hipLaunchKernelGGL((fa_bwd_di_kernel<D>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, O,
+                     G, di, rows);
+  const int nb = (N + kBlk - 1) / kBlk;
+  const int total = (int)(BH * nb);
+  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL>), dim3(total), dim3(256), 0, s, Q, K, V, G, lse,
+                     di, dk, dv, N, nb, total, c, scale);
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL>), dim3(total), dim3(256), 0, s, Q, K, V, G, lse,
+                     di, dq, N, nb, total, c, scale);
+  return hipGetLastError();
+}
+
+}  // namespace bwd
+}  // namespace fa
+
+extern "C" int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N) {
+  if (B <= 0 || H <= 0 || N <= 0) return 0;
+  return B * H * N;
+}
+
+extern "C" int fa_bwd_f16(const void* q, const void* k, const void* v, const void* o,
+                          const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                          float* workspace, int64_t B, int64_t H, int64_t N, int64_t D, int causal,
+                          void* stream) {
+  using namespace fa::bwd;
+  const int st = fa_validate_bwd(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, N, D);
+  if (st != FA_OK) return st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t BH = B * H;
+  hipError_t e;
+  if (D == 64) {
+    e = causal ? launch_bwd<64, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s)
+               : launch_bwd<64, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s);
+  } else {
+    e = causal ? launch_bwd<128, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s)
+               : launch_bwd<128, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s);
+  }
+  return e == hipSuccess ? FA_OK : -(int)e;
+}

@@ -57,6 +57,28 @@ extern "C" int fa_validate_fwd(const void* q, const void* k, const void* v, cons
   return FA_OK;
 }
 
+// Mirrors the reference backward launcher's checks (cuda/flash_attn_kernel.cu:
+// 425-432: CUDA tensors, head dimension), widened to D in {64, 128}, plus the
+// C ABI's own pointer, alignment and index-range checks.
+extern "C" int fa_validate_bwd(const void* q, const void* k, const void* v, const void* o,
+                               const void* dout, const float* lse, const float* dq,
+                               const float* dk, const float* dv, const float* workspace,
+                               int64_t B, int64_t H, int64_t N, int64_t D) {
+  if (!dout || !lse || !dq || !dk || !dv || !workspace) return FA_ERR_NULL_POINTER;
+  const int st = fa_validate_fwd(q, k, v, o, B, H, N, D);
+  if (st != FA_OK) return st;
+  if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return FA_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(lse) & 3u) != 0 ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
+    return FA_ERR_ALIGNMENT;
+  // The row-sum kernel's grid (32 rows per workgroup) and the per-head float
+  // offsets of the gradients.
+  if (B * H > kMaxGrid / N) return FA_ERR_TOO_LARGE;
+  if ((B * H * N + 31) / 32 > kMaxGrid) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
 extern "C" int fa_validate_decode(const void* q, const void* k_pool, const void* v_pool,
                                   const int32_t* page_table, const int32_t* ctx_lens,
                                   int64_t B, int64_t H, int64_t D, int64_t page_size,

@@ -204,7 +204,8 @@ struct RowBlock {
   template <int NB>
   __device__ __forceinline__ void softmax_keep(const f32x16 (&s)[NB], f16x8 (&pf)[2 * NB]) {
     float rs = expo_pack<NB>(s, pf, m_run);
-    if (!__all(rs <= kSumLimit)) rs = rescue<NB>(s, pf);
+    // Rare: the merge copies of P, O and l go on this edge, not the fast one.
+    if (__builtin_expect(!__all(rs <= kSumLimit), 0)) rs = rescue<NB>(s, pf);
     l_run += rs;
   }
 
@@ -1137,7 +1138,7 @@ extern "C" int fa_probe_default_variant(int64_t D) {
 }
 
 extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D) {
-  static const int all[] = {12, 13, 14, 22, 23, 24, 42, 112, 113, 114, 122, 123, 204};
+  static const int all[] = {12, 13, 14, 22, 23, 24, 42, 121, 131, 141, 122, 132, 204};
   int n = 0;
   for (int v : all) {
     if (fa::variant_fits((int)D, v)) {

@@ -84,6 +84,14 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds, ui
                :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(r)
                : "memory", "m0");
 }
+
+// 4 bytes per lane from global (rsrc + voffset) into LDS at byte lds + 4*lane;
+// the dword form needs only 4-byte alignment of the source.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(r)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // s_waitcnt vmcnt(0) through the builtin, so the compiler also knows that its

@@ -3,6 +3,8 @@
 // Mirrors the reference module built from cuda/flash_attn_fa3_db_full.cu:
 //   forward(Q, K, V)      -> [O half [B,H,N,D], L float [B,H,N]]   (:405-408)
 //   forward_only(Q, K, V) -> O                                      (:410-413)
+// and the backward of the reference's first module (cuda/flash_attn_kernel.cu):
+//   backward(Q, K, V, O, dO, L) -> [dQ, dK, dV] float [B,H,N,D]     (:417-503)
 // with the same argument checks and messages as fa3db_full_forward_impl
 // (:352-363), the same fp16 cast of the inputs (:366-368), fresh outputs on
 // Q's device (:370-376) and an asynchronous launch on the current stream
@@ -73,6 +75,50 @@ std::vector<torch::Tensor> forward(torch::Tensor Q, torch::Tensor K, torch::Tens
 
 torch::Tensor forward_only(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal) {
   return forward_impl(Q, K, V, /*want_L=*/false, causal).first;
+}
+
+// backward(Q, K, V, O, dO, L) -> [dQ, dK, dV] float32 [B,H,N,D], the module
+// function of cuda/flash_attn_kernel.cu:417-503 (checks :425-432). Q/K/V/O/dO
+// are cast to fp16 (O from forward() already is), L to fp32; the D_i
+// workspace comes from the caching allocator.
+std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                    torch::Tensor O, torch::Tensor dO, torch::Tensor L,
+                                    bool causal) {
+  TORCH_CHECK(Q.is_cuda(), "Q must be a CUDA tensor");
+  TORCH_CHECK(dO.is_cuda(), "dO must be a CUDA tensor");
+  TORCH_CHECK(K.is_cuda() && V.is_cuda() && O.is_cuda() && L.is_cuda(),
+              "K/V/O/L must be CUDA tensors");
+  TORCH_CHECK(Q.dim() == 4, "Q must be 4D [B, H, N, D]");
+  const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
+  TORCH_CHECK(D == 64 || D == 128, "Head dimension must be 64 or 128");
+  TORCH_CHECK(N > 0, "N must be > 0");
+  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
+                  dO.sizes() == Q.sizes(),
+              "K, V, O and dO must have the same shape as Q");
+  TORCH_CHECK(L.numel() == B * H * N, "L must hold B*H*N logsumexp values");
+  const auto dev = Q.device();
+  TORCH_CHECK(K.device() == dev && V.device() == dev && O.device() == dev && dO.device() == dev &&
+                  L.device() == dev,
+              "Q/K/V/O/dO/L must be on the same device");
+
+  const c10::DeviceGuard guard(dev);
+  const int64_t BH = B * H;
+  auto half = [&](const torch::Tensor& t) {
+    return t.to(torch::kHalf).reshape({BH, N, D}).contiguous();
+  };
+  auto Qh = half(Q), Kh = half(K), Vh = half(V), Oh = half(O), dOh = half(dO);
+  auto Lf = L.to(torch::kFloat).reshape({BH, N}).contiguous();
+  auto f32 = Qh.options().dtype(torch::kFloat);
+  auto dQ = torch::empty({B, H, N, D}, f32);
+  auto dK = torch::empty({B, H, N, D}, f32);
+  auto dV = torch::empty({B, H, N, D}, f32);
+  auto ws = torch::empty({fa_bwd_workspace_floats(B, H, N)}, f32);
+  const int st = fa_bwd_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), Oh.data_ptr(),
+                            dOh.data_ptr(), Lf.data_ptr<float>(), dQ.data_ptr<float>(),
+                            dK.data_ptr<float>(), dV.data_ptr<float>(), ws.data_ptr<float>(), B, H,
+                            N, D, causal ? 1 : 0, current_stream(Qh));
+  check_status(st, "fa_bwd_f16");
+  return {dQ, dK, dV};
 }
 
 // Test support: the forward through one explicit kernel variant.
@@ -256,6 +302,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
   m.def("forward_only", &forward_only, "FlashAttention forward, O only",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
+  m.def("backward", &backward, "FlashAttention backward: returns [dQ, dK, dV] float",
+        py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("dO"), py::arg("L"),
+        py::arg("causal") = false);
   m.def("decode_paged", &decode_paged, "split-KV paged decode: returns [O half, L float]",
         py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("page_table"),
         py::arg("ctx_lens"), py::arg("num_splits") = 16);

@@ -75,6 +75,34 @@ int fa_fwd_f16(const void* q, const void* k, const void* v, void* o, float* lse,
                void* stream);
 
 /*
+ * Host-only argument check of fa_bwd_f16. Replaces the checks of the reference
+ * backward launcher flash_attn_backward (cuda/flash_attn_kernel.cu:425-432),
+ * widened to D in {64, 128}.
+ */
+int fa_validate_bwd(const void* q, const void* k, const void* v, const void* o,
+                    const void* dout, const float* lse, const float* dq, const float* dk,
+                    const float* dv, const float* workspace, int64_t B, int64_t H,
+                    int64_t N, int64_t D);
+
+/* Floats of the workspace fa_bwd_f16 needs: B*H*N (the row sums D_i). */
+int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N);
+
+/*
+ * Attention backward from the forward's outputs: given q, k, v, o (fp16
+ * [B,H,N,D]), dout = dL/do (fp16 [B,H,N,D]) and lse (fp32 [B,H,N], the
+ * forward's natural-log logsumexp), writes fp32 [B,H,N,D] gradients
+ *   dq = dS k / sqrt(D),  dk = dS^T q / sqrt(D),  dv = P^T dout,
+ * with P = exp(q k^T / sqrt(D) - lse) [causal-masked], dS = P * (dout v^T - D_i),
+ * D_i = rowsum(dout * o). workspace: caller-provided fp32 [B*H*N].
+ * Replaces flash_attn_backward (cuda/flash_attn_kernel.cu:417-503), which
+ * takes the same six tensors (fp32 there) and returns [dQ, dK, dV]; the causal
+ * flag and D = 128 have no reference counterpart.
+ */
+int fa_bwd_f16(const void* q, const void* k, const void* v, const void* o, const void* dout,
+               const float* lse, float* dq, float* dk, float* dv, float* workspace,
+               int64_t B, int64_t H, int64_t N, int64_t D, int causal, void* stream);
+
+/*
  * Host-only argument check of the decode entry points. No reference
  * counterpart (the reference has no decode path).
  */

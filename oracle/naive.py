@@ -33,6 +33,9 @@ Pinning status (each function is checked in tests/test_oracle.py):
   over the contiguous keys; gather equals a direct index walk.
 * split_partials + lse_combine: combine of any split count equals the
   unsplit result; one split is the identity; empty splits carry weight 0.
+* naive_attention_backward (tests/test_backward.py:20-46): float64 central
+  finite differences of sum(naive_attention(Q, K, V) * dO) in every input
+  element, causal and not, on tiny inputs.
 """
 from __future__ import annotations
 
@@ -91,6 +94,47 @@ def naive_attention(Q, K, V, causal: bool = False, dtype=np.float32):
             O[b, h] = P @ V[b, h]
             L[b, h] = l
     return O, L
+
+
+def naive_attention_backward(Q, K, V, dO, causal: bool = False, dtype=np.float32):
+    """dQ, dK, dV of naive attention (tests/test_backward.py:20-46).
+
+    Restates the reference's naive backward step by step, per (b, h):
+        S  = Q K^T * scale (+ causal mask)          (:23-24)
+        P  = softmax(S); O = P V                    (:25-26)
+        dV = P^T dO                                 (:29)
+        dP = dO V^T                                 (:32)
+        Di = rowsum(dO * O)                         (:35)
+        dS = P * (dP - Di)                          (:38)
+        dQ = dS K * scale; dK = dS^T Q * scale      (:41, :44)
+    in ``dtype`` on the given inputs (the GPU path's inputs are fp16, so the
+    tests pass half-cast arrays). Pinned by a float64 finite-difference check
+    of ``naive_attention`` in tests/test_oracle.py.
+    """
+    Q = np.asarray(Q, dtype=dtype)
+    K = np.asarray(K, dtype=dtype)
+    V = np.asarray(V, dtype=dtype)
+    dO = np.asarray(dO, dtype=dtype)
+    B, H, N, D = Q.shape
+    scale = dtype(D ** -0.5) if dtype is not np.float64 else D ** -0.5
+    dQ = np.empty_like(Q)
+    dK = np.empty_like(K)
+    dV = np.empty_like(V)
+    mask = np.arange(N)[None, :] > np.arange(N)[:, None] if causal else None
+    for b in range(B):
+        for h in range(H):
+            S = (Q[b, h] @ K[b, h].T) * scale
+            if mask is not None:
+                S = np.where(mask, -np.inf, S).astype(dtype)
+            P, _ = _softmax_lse(S)
+            O = P @ V[b, h]
+            dV[b, h] = P.T @ dO[b, h]
+            dP = dO[b, h] @ V[b, h].T
+            Di = (dO[b, h] * O).sum(axis=-1, keepdims=True)
+            dS = P * (dP - Di)
+            dQ[b, h] = (dS @ K[b, h]) * scale
+            dK[b, h] = (dS.T @ Q[b, h]) * scale
+    return dQ, dK, dV
 
 
 def attention_bruteforce(q, k, v, causal: bool = False):

@@ -111,3 +111,49 @@ def test_package_loads_native_libraries(fa):
     libs = fa.loaded_libraries()
     assert any(p.endswith("libfa_mi355x.so") for p in libs)
     assert any("_fa_torch" in p for p in libs)
+
+
+def _bwd(**kw):
+    b = dict(q=A, k=A, v=A, o=A, do=A, lse=A, dq=A, dk=A, dv=A, ws=A, B=1, H=8, N=4096, D=64)
+    b.update(kw)
+    return tuple(b[k] for k in ("q", "k", "v", "o", "do", "lse", "dq", "dk", "dv", "ws",
+                                "B", "H", "N", "D"))
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), "FA_OK"),
+    (dict(D=128, B=4, H=16), "FA_OK"),
+    (dict(N=1), "FA_OK"),
+    (dict(do=0), "FA_ERR_NULL_POINTER"),
+    (dict(lse=0), "FA_ERR_NULL_POINTER"),
+    (dict(ws=0), "FA_ERR_NULL_POINTER"),
+    (dict(dv=0), "FA_ERR_NULL_POINTER"),
+    (dict(q=0), "FA_ERR_NULL_POINTER"),
+    (dict(D=96), "FA_ERR_HEAD_DIM"),
+    (dict(N=0), "FA_ERR_SEQ_LEN"),
+    (dict(H=0), "FA_ERR_BATCH_HEADS"),
+    (dict(do=A + 8), "FA_ERR_ALIGNMENT"),
+    (dict(dk=A + 4), "FA_ERR_ALIGNMENT"),
+    (dict(lse=A + 2), "FA_ERR_ALIGNMENT"),
+    (dict(lse=A + 4), "FA_OK"),
+    (dict(B=1 << 20, H=1 << 20, N=128), "FA_ERR_TOO_LARGE"),
+])
+def test_validate_bwd(capi, kw, code):
+    lib = capi.load()
+    assert lib.fa_validate_bwd(*_bwd(**kw)) == capi.STATUS[code]
+
+
+def test_bwd_rejects_before_touching_the_device(capi):
+    lib = capi.load()
+    assert lib.fa_bwd_f16(*_bwd(D=80), 0, None) == capi.STATUS["FA_ERR_HEAD_DIM"]
+    assert lib.fa_bwd_f16(*_bwd(ws=0), 1, None) == capi.STATUS["FA_ERR_NULL_POINTER"]
+    assert lib.fa_bwd_workspace_floats(2, 8, 4096) == 2 * 8 * 4096
+    assert lib.fa_bwd_workspace_floats(0, 8, 4096) == 0
+
+
+def test_torch_backward_checks_mirror_reference(fa):
+    """The reference checks Q then dO for is_cuda (cuda/flash_attn_kernel.cu:425-426)."""
+    import torch
+    x = torch.zeros(1, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="Q must be a CUDA tensor"):
+        fa.backward(x, x, x, x, x, torch.zeros(1, 1, 8))

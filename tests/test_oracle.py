@@ -291,3 +291,101 @@ def test_planted_combine_mistake_is_caught():
     w = np.where(np.isfinite(Ls), np.exp(Ls - M), 0)
     bad = (w[..., None] * Os).sum(-2) / np.isfinite(Ls).sum(-1, keepdims=True)
     assert not np.allclose(bad, z["o"], atol=1e-6)
+
+
+# ---------------------------------------------------------------- backward
+def _fd_grads(Q, K, V, G, causal, eps=1e-6):
+    """Central finite differences of sum(naive_attention(Q, K, V) * G), float64."""
+    def loss(q, k, v):
+        O, _ = orc.naive_attention(q, k, v, causal, np.float64)
+        return float((O * G).sum())
+
+    out = []
+    for which in range(3):
+        args = [Q.copy(), K.copy(), V.copy()]
+        g = np.zeros_like(args[which])
+        for idx in np.ndindex(*g.shape):
+            a = args[which]
+            keep = a[idx]
+            a[idx] = keep + eps
+            hi = loss(*args)
+            a[idx] = keep - eps
+            lo = loss(*args)
+            a[idx] = keep
+            g[idx] = (hi - lo) / (2 * eps)
+        out.append(g)
+    return out
+
+
+def _bwd_inputs(seed, B=1, H=2, N=6, D=4):
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal((B, H, N, D)) for _ in range(4)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_matches_finite_differences(causal):
+    Q, K, V, G = _bwd_inputs(7)
+    ref = _fd_grads(Q, K, V, G, causal)
+    got = orc.naive_attention_backward(Q, K, V, G, causal, np.float64)
+    for name, r, g in zip("QKV", ref, got):
+        np.testing.assert_allclose(g, r, atol=1e-7, rtol=1e-6, err_msg=f"d{name}")
+    # float32 (the tests' precision) stays within 1e-5 of float64
+    got32 = orc.naive_attention_backward(Q, K, V, G, causal)
+    for g32, g in zip(got32, got):
+        np.testing.assert_allclose(g32, g, atol=1e-5)
+
+
+def test_backward_closed_forms():
+    Q, K, V, G = _bwd_inputs(8, N=5)
+    dQ, dK, dV = orc.naive_attention_backward(Q, K, V, G, False, np.float64)
+    # sum over keys of dS is zero per row, so sum_j dK_j = 0 and the gradient
+    # with respect to a common shift of all keys vanishes
+    np.testing.assert_allclose(dK.sum(axis=2), 0, atol=1e-12)
+    # dV columns sum to the dO columns (P rows sum to one)
+    np.testing.assert_allclose(dV.sum(axis=2), G.sum(axis=2), atol=1e-12)
+    # causal: row 0 attends only key 0, so dQ[0] = 0 and dV[0] gets dO[0] in full
+    dQc, dKc, dVc = orc.naive_attention_backward(Q, K, V, G, True, np.float64)
+    np.testing.assert_allclose(dQc[:, :, 0], 0, atol=1e-12)
+    # the last key is seen only by the last query: dV[N-1] = P[N-1, N-1] * dO[N-1]
+    # with P[N-1, N-1] = exp(q.k / sqrt(4) - L[N-1])
+    s = (Q[:, :, -1] * K[:, :, -1]).sum(-1) / 2.0 - orc.naive_attention(
+        Q, K, V, True, np.float64)[1][:, :, -1]
+    np.testing.assert_allclose(dVc[:, :, -1], np.exp(s)[..., None] * G[:, :, -1], atol=1e-12)
+
+
+def _mut_bwd_no_di(Q, K, V, dO, causal=False, dtype=np.float64):     # dS = P * dP
+    Q, K, V, dO = (np.asarray(a, dtype) for a in (Q, K, V, dO))
+    dQ, dK, dV = orc.naive_attention_backward(Q, K, V, dO, causal, dtype)
+    O, _ = orc.naive_attention(Q, K, V, causal, dtype)
+    Di = (dO * O).sum(-1, keepdims=True)
+    # adding back P * Di through dQ = dS K scale drops the -Di term
+    S = np.einsum("bhid,bhjd->bhij", Q, K) * Q.shape[-1] ** -0.5
+    if causal:
+        S = np.where(np.arange(S.shape[-1])[None, :] > np.arange(S.shape[-2])[:, None], -np.inf, S)
+    P, _ = orc._softmax_lse(S)
+    return dQ + np.einsum("bhij,bhjd->bhid", P * Di, K) * Q.shape[-1] ** -0.5, dK, dV
+
+
+def _mut_bwd_dk_unscaled(Q, K, V, dO, causal=False, dtype=np.float64):  # dK without scale
+    dQ, dK, dV = orc.naive_attention_backward(Q, K, V, dO, causal, dtype)
+    return dQ, dK * Q.shape[-1] ** 0.5, dV
+
+
+def _mut_bwd_dv_untransposed(Q, K, V, dO, causal=False, dtype=np.float64):  # dV = P dO
+    S = np.einsum("bhid,bhjd->bhij", Q, K) * Q.shape[-1] ** -0.5
+    if causal:
+        S = np.where(np.arange(S.shape[-1])[None, :] > np.arange(S.shape[-2])[:, None], -np.inf, S)
+    P, _ = orc._softmax_lse(S)
+    dQ, dK, _ = orc.naive_attention_backward(Q, K, V, dO, causal, dtype)
+    return dQ, dK, np.einsum("bhij,bhjd->bhid", P, dO)
+
+
+@pytest.mark.parametrize("mut", [_mut_bwd_no_di, _mut_bwd_dk_unscaled, _mut_bwd_dv_untransposed])
+def test_planted_backward_mistakes_are_caught(mut):
+    Q, K, V, G = _bwd_inputs(9, N=5)
+    for causal in (False, True):
+        ref = _fd_grads(Q, K, V, G, causal)
+        got = mut(Q, K, V, G, causal)
+        if not all(np.allclose(g, r, atol=1e-6, rtol=1e-6) for g, r in zip(got, ref)):
+            return
+    pytest.fail("finite differences did not catch the planted mistake")
