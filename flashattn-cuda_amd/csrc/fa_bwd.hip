@@ -28,6 +28,7 @@
 #include <math.h>
 #include <stdint.h>
 
+
 #include "fa_mi355x.h"
 #include "fa_tile.hpp"
 
@@ -125,12 +126,14 @@ __device__ __forceinline__ void store_transposed(float* out, int n, int row0, in
 }
 
 // ---------------------------------------------------------------------------
-// D_i = sum_d dO[i][d] * O[i][d]; 8 lanes per row, one 16-byte chunk each per
-// step (coalesced 128-byte runs), reduced with DPP-free xor shuffles.
+// Row terms: Di[i] = sum_d dO[i][d] * O[i][d] and NL[i] = -L[i] * log2(e)
+// (so that P = exp2(S c + NL) takes one fma). 8 lanes per row, one 16-byte
+// chunk each per step (coalesced 128-byte runs), reduced with xor shuffles.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ void __launch_bounds__(256)
-fa_bwd_di_kernel(const f16* __restrict__ O, const f16* __restrict__ dO, float* __restrict__ Di,
+fa_bwd_di_kernel(const f16* __restrict__ O, const f16* __restrict__ dO,
+                 const float* __restrict__ L, float* __restrict__ Di, float* __restrict__ NL,
                  int64_t rows) {
   const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
   const int part = threadIdx.x & 7;
@@ -148,61 +151,98 @@ fa_bwd_di_kernel(const f16* __restrict__ O, const f16* __restrict__ dO, float* _
   acc += __shfl_xor(acc, 1, 8);
   acc += __shfl_xor(acc, 2, 8);
   acc += __shfl_xor(acc, 4, 8);
-  if (row < rows && part == 0) Di[row] = acc;
+  if (row < rows && part == 0) {
+    Di[row] = acc;
+    NL[row] = -L[row] * kLog2e;
+  }
+}
+
+// Partial accumulators of the second wave group, added into the first's
+// through LDS (lane-major, conflict-free): wave slot w, NA arrays of DB
+// blocks of 16 registers.
+template <int NA, int DB>
+__device__ __forceinline__ void group_reduce(char* smem, int grp, int slot, int lane,
+                                             f32x16 (&a)[NA][DB]) {
+  float* buf = reinterpret_cast<float*>(smem) + (size_t)slot * NA * DB * 16 * 64 + lane;
+  __syncthreads();   // every wave is done with the staging buffers
+  if (grp == 1) {
+#pragma unroll
+    for (int x = 0; x < NA; ++x)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) buf[((x * DB + db) * 16 + r) * 64] = a[x][db][r];
+  }
+  __syncthreads();
+  if (grp == 0) {
+#pragma unroll
+    for (int x = 0; x < NA; ++x)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a[x][db][r] += buf[((x * DB + db) * 16 + r) * 64];
+  }
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV. Workgroup = 4 waves = 128 keys of one (b, h); wave w owns keys
-// k0 + 32 w .. +31. Query tiles of 64 rows stream through 2 LDS stages; each
-// stage holds Q and dO twice (row swizzle, transposed swizzle) and 64 floats
-// each of L and D_i.
+// dK, dV. Workgroup = 4 G waves, 128 keys of one (b, h): wave w owns keys
+// k0 + 32 (w % 4) .. +31 and, with G = 2, query half w / 4 of every tile (the
+// two groups' partial sums are added at the end). Query tiles of 64 rows
+// stream through 2 LDS stages; each stage holds Q and dO twice (row swizzle,
+// transposed swizzle) and 64 floats each of NL and D_i.
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(256)
+template <int D, bool CAUSAL, int G>
+__global__ void __launch_bounds__(256 * G)
 fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, const f16* __restrict__ dO,
-                   const float* __restrict__ L, const float* __restrict__ Di,
+                   const float* __restrict__ NL, const float* __restrict__ Di,
                    float* __restrict__ dK, float* __restrict__ dV, int N, int num_kb, int total,
                    float c, float scale) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
-  constexpr int STAGE = 4 * TILE + 2048;       // Qk | Qv | dOk | dOv | L | D_i
-  constexpr int LOADS = 4 * BLOCKS / 4;        // tile blocks per wave per stage
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  constexpr int STAGE = 4 * TILE + 2048;       // Qk | Qv | dOk | dOv | NL | D_i
+  constexpr int WAVES = 4 * G;
+  constexpr int LOADS = 4 * BLOCKS / WAVES;    // tile blocks per wave per stage
+  constexpr int SMEM = 2 * STAGE > (G - 1) * 4 * 2 * DB * 16 * 64 * 4
+                           ? 2 * STAGE : (G - 1) * 4 * 2 * DB * 16 * 64 * 4;
+  static_assert(4 * BLOCKS % WAVES == 0, "copy blocks split evenly over the waves");
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kw = wave & 3;
+  const int grp = wave >> 2;
   const int hi = lane >> 5;
   const int logical = xcd_remap(blockIdx.x, total);
   const int bh = logical / num_kb;
   const int kb = logical - bh * num_kb;
   const int k0 = kb * kBlk;
-  const int key = k0 + 32 * wave + (lane & 31);
+  const int key = k0 + 32 * kw + (lane & 31);
 
   const size_t head = (size_t)bh * N * D;
   const int head_bytes = N * D * 2;
   const char* Qh = reinterpret_cast<const char*>(Q + head);
   const char* Gh = reinterpret_cast<const char*>(dO + head);
-  const float* Lh = L + (size_t)bh * N;
+  const float* Lh = NL + (size_t)bh * N;
   const float* Dh = Di + (size_t)bh * N;
 
   f16x8 kf[KSTEPS], vf[KSTEPS];   // B operands: K^T and V^T of this wave's keys
-  load_row_operand<D>(K + head, N, k0 + 32 * wave, lane, kf);
-  load_row_operand<D>(V + head, N, k0 + 32 * wave, lane, vf);
-  f32x16 dv[DB], dk[DB];
+  load_row_operand<D>(K + head, N, k0 + 32 * kw, lane, kf);
+  load_row_operand<D>(V + head, N, k0 + 32 * kw, lane, vf);
+  f32x16 acc[2][DB];              // [0] = dV^T, [1] = dK^T (unscaled)
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
-    dv[db] = f32x16{};
-    dk[db] = f32x16{};
+    acc[0][db] = f32x16{};
+    acc[1][db] = f32x16{};
   }
 
-  // Block i of this wave's share of a stage: part (i*4 + wave) / BLOCKS of
-  // {Qk, Qv, dOk, dOv}, block (i*4 + wave) % BLOCKS of that tile.
+  // Block b = i * WAVES + wave of a stage: part b / BLOCKS of {Qk, Qv, dOk,
+  // dOv}, block b % BLOCKS of that tile.
   uint32_t off[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
-    const int b = i * 4 + wave;
+    const int b = i * WAVES + wave;
     uint32_t ko, vo;
     block_offsets<D>(b % BLOCKS, lane, ko, vo);
     off[i] = ((b / BLOCKS) & 1) ? vo : ko;
@@ -212,13 +252,66 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     const uint32_t base = lds0 + st * STAGE;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int b = i * 4 + wave;
+      const int b = i * WAVES + wave;
       const int part = b / BLOCKS;
       copy_block<D>(part < 2 ? Qh : Gh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
                     off[i]);
     }
     if (wave == 0) copy_rowvec(Lh, N, t, base + 4 * TILE, lane);
     if (wave == 1) copy_rowvec(Dh, N, t, base + 4 * TILE + 1024, lane);
+  };
+
+  // One 32-query block qb of the tile at sb: S = Q K^T and dP = dO V^T
+  // (C layout: register r holds query qt0 + 32 qb + 8 (r/4) + 4 hi + r%4,
+  // lane l key l%32), then P, dS and the two gradient products. `mid` runs
+  // once the score products are issued (the next tile's copies go there, so
+  // their issue overlaps the matrix cores).
+  auto body = [&](const char* sb, int qt0, int qb, bool edge, auto mid) {
+    const char* qk = sb;
+    const char* qv = sb + TILE;
+    const char* gk = sb + 2 * TILE;
+    const char* gv = sb + 3 * TILE;
+    const float* ls = reinterpret_cast<const float*>(sb + 4 * TILE);
+    const float* ds = reinterpret_cast<const float*>(sb + 4 * TILE + 1024);
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      s = mfma32(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
+      dp = mfma32(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
+    }
+    mid();
+    f32x16 p, g;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4 lq = *reinterpret_cast<const f32x4*>(ls + 32 * qb + 8 * r4 + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[4 * r4 + e] = exp2_hw(fmaf(s[4 * r4 + e], c, lq[e]));
+    }
+    if (edge) {   // rows past N, and (causal) keys after the row
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int q = qt0 + 32 * qb + 8 * (r >> 2) + 4 * hi + (r & 3);
+        p[r] = ((q >= N) || (CAUSAL && key > q)) ? 0.f : p[r];
+      }
+    }
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4 dq = *reinterpret_cast<const f32x4*>(ds + 32 * qb + 8 * r4 + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g[4 * r4 + e] = p[4 * r4 + e] * (dp[4 * r4 + e] - dq[e]);
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS over the two 16-query k-steps.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * qb + h;
+      const f16x8 pb = pack_p(p, h);
+      const f16x8 gb = pack_p(g, h);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        acc[0][db] = mfma32(load_v_frag<D>(gv, j, db, lane), pb, acc[0][db]);
+        acc[1][db] = mfma32(load_v_frag<D>(qv, j, db, lane), gb, acc[1][db]);
+      }
+    }
   };
 
   const int n_qt = (N + kBQ - 1) / kBQ;
@@ -230,91 +323,65 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   }
   for (int t = t0; t < n_qt; ++t) {
     const int st = (t - t0) & 1;
-    if (t + 1 < n_qt) issue(t + 1, st ^ 1);
     const char* sb = smem + st * STAGE;
-    const char* qk = sb;
-    const char* qv = sb + TILE;
-    const char* gk = sb + 2 * TILE;
-    const char* gv = sb + 3 * TILE;
-    const float* ls = reinterpret_cast<const float*>(sb + 4 * TILE);
-    const float* ds = reinterpret_cast<const float*>(sb + 4 * TILE + 1024);
     const int qt0 = t * kBQ;
+    auto prefetch = [&] {
+      if (t + 1 < n_qt) issue(t + 1, st ^ 1);
+    };
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      // S and dP for 32 queries x this wave's 32 keys; C layout: register r
-      // holds query qt0 + 32 qb + 8 (r/4) + 4 hi + r%4, lane l key l%32.
-      f32x16 s = {}, dp = {};
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
-        s = mfma32(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
-        dp = mfma32(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
-      }
-      f32x16 p, g;
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int qo = 32 * qb + 8 * r4 + 4 * hi;
-        const f32x4 lq = *reinterpret_cast<const f32x4*>(ls + qo);
-        const f32x4 dq = *reinterpret_cast<const f32x4*>(ds + qo);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * r4 + e;
-          const int q = qt0 + qo + e;
-          float pv = exp2_hw(fmaf(s[r], c, -lq[e] * kLog2e));
-          const bool dead = (q >= N) || (CAUSAL && key > q);
-          pv = dead ? 0.f : pv;
-          p[r] = pv;
-          g[r] = pv * (dp[r] - dq[e]);
-        }
-      }
-      // dV^T += dO^T P and dK^T += Q^T dS over the two 16-query k-steps.
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int j = 2 * qb + h;
-        const f16x8 pb = pack_p(p, h);
-        const f16x8 gb = pack_p(g, h);
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          dv[db] = mfma32(load_v_frag<D>(gv, j, db, lane), pb, dv[db]);
-          dk[db] = mfma32(load_v_frag<D>(qv, j, db, lane), gb, dk[db]);
-        }
-      }
+    for (int i = 0; i < 2 / G; ++i) {
+      const int qb = G == 2 ? grp : i;
+      // masking only where a query is past N or precedes one of the keys
+      const bool edge = (qt0 + 32 * qb + 32 > N) ||
+                        (CAUSAL && qt0 + 32 * qb < k0 + 32 * kw + 32);
+      if (i == 0) body(sb, qt0, qb, edge, prefetch);
+      else body(sb, qt0, qb, edge, [] {});
     }
     wait_vmem();
     __syncthreads();
   }
-  store_transposed<D>(dV + head, N, k0 + 32 * wave, lane, dv, 1.f);
-  store_transposed<D>(dK + head, N, k0 + 32 * wave, lane, dk, scale);
+  if constexpr (G == 2) group_reduce<2, DB>(smem, grp, kw, lane, acc);
+  if (grp == 0) {
+    store_transposed<D>(dV + head, N, k0 + 32 * kw, lane, acc[0], 1.f);
+    store_transposed<D>(dK + head, N, k0 + 32 * kw, lane, acc[1], scale);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// dQ. Workgroup = 4 waves = 128 queries of one (b, h); wave w owns queries
-// q0 + 32 w .. +31 (Q^T and dO^T as register B operands, L and D_i as lane
-// constants). Key tiles of 64 rows stream through 2 LDS stages, each holding
-// K twice (row swizzle, transposed swizzle) and V once (row swizzle).
+// dQ. Workgroup = 4 G waves, 128 queries of one (b, h): wave w owns queries
+// q0 + 32 (w % 4) .. +31 (Q^T and dO^T as register B operands, NL and D_i as
+// lane constants) and, with G = 2, key half w / 4 of every tile. Key tiles of
+// 64 rows stream through 2 LDS stages, each holding K twice (row swizzle,
+// transposed swizzle) and V once (row swizzle).
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(256)
+template <int D, bool CAUSAL, int G>
+__global__ void __launch_bounds__(256 * G)
 fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, const f16* __restrict__ dO,
-                 const float* __restrict__ L, const float* __restrict__ Di,
+                 const float* __restrict__ NL, const float* __restrict__ Di,
                  float* __restrict__ dQ, int N, int num_qb, int total, float c, float scale) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
   constexpr int STAGE = 3 * TILE;              // Kk | Kv | Vk
   constexpr int NBLK = 3 * BLOCKS;
-  constexpr int LOADS = (NBLK + 3) / 4;        // tile blocks per wave per stage (some idle)
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  constexpr int WAVES = 4 * G;
+  constexpr int LOADS = (NBLK + WAVES - 1) / WAVES;   // tile blocks per wave per stage
+  constexpr int SMEM = 2 * STAGE > (G - 1) * 4 * DB * 16 * 64 * 4
+                           ? 2 * STAGE : (G - 1) * 4 * DB * 16 * 64 * 4;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qw = wave & 3;
+  const int grp = wave >> 2;
   const int hi = lane >> 5;
   const int logical = xcd_remap(blockIdx.x, total);
   const int bh = logical / num_qb;
   int qb = logical - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows first
   const int q0 = qb * kBlk;
-  const int query = q0 + 32 * wave + (lane & 31);
+  const int query = q0 + 32 * qw + (lane & 31);
 
   const size_t head = (size_t)bh * N * D;
   const int head_bytes = N * D * 2;
@@ -322,19 +389,19 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const char* Vh = reinterpret_cast<const char*>(V + head);
 
   f16x8 qf[KSTEPS], gf[KSTEPS];   // B operands: Q^T and dO^T of this wave's queries
-  load_row_operand<D>(Q + head, N, q0 + 32 * wave, lane, qf);
-  load_row_operand<D>(dO + head, N, q0 + 32 * wave, lane, gf);
+  load_row_operand<D>(Q + head, N, q0 + 32 * qw, lane, qf);
+  load_row_operand<D>(dO + head, N, q0 + 32 * qw, lane, gf);
   const bool row_ok = query < N;
-  const float lq = row_ok ? L[(size_t)bh * N + query] * kLog2e : 0.f;
+  const float nl = row_ok ? NL[(size_t)bh * N + query] : 0.f;
   const float dq_i = row_ok ? Di[(size_t)bh * N + query] : 0.f;
-  f32x16 acc[DB];
+  f32x16 acc[1][DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  for (int db = 0; db < DB; ++db) acc[0][db] = f32x16{};
 
   uint32_t off[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
-    const int b = i * 4 + wave;
+    const int b = i * WAVES + wave;
     uint32_t ko, vo;
     block_offsets<D>(b % BLOCKS, lane, ko, vo);
     off[i] = ((b / BLOCKS) == 1) ? vo : ko;
@@ -344,7 +411,7 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     const uint32_t base = lds0 + st * STAGE;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int b = i * 4 + wave;
+      const int b = i * WAVES + wave;
       if (b < NBLK) {   // wave-uniform
         const int part = b / BLOCKS;
         copy_block<D>(part < 2 ? Kh : Vh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
@@ -353,55 +420,85 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     }
   };
 
+  // One 32-key half of the tile at kt: S^T = K Q^T and dP^T = V dO^T
+  // (register r holds key kt0 + 32 half + 8 (r/4) + 4 hi + r%4, lane l query
+  // l%32), then dS^T and dQ^T += K^T dS^T. `mid` runs once the score
+  // products are issued.
+  auto body = [&](const char* kt, int kt0, int half, bool edge, auto mid) {
+    const char* kk_t = kt;
+    const char* kv_t = kt + TILE;
+    const char* vk_t = kt + 2 * TILE;
+    f32x16 s = {}, dp = {};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      s = mfma32(load_k_frag<D>(kk_t, half, kk, lane), qf[kk], s);
+      dp = mfma32(load_k_frag<D>(vk_t, half, kk, lane), gf[kk], dp);
+    }
+    mid();
+    f32x16 p;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = exp2_hw(fmaf(s[r], c, nl));
+    if (edge) {   // keys past N, rows past N, and (causal) keys after the row
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kidx = kt0 + 32 * half + 8 * (r >> 2) + 4 * hi + (r & 3);
+        p[r] = ((kidx >= N) || (CAUSAL && kidx > query) || !row_ok) ? 0.f : p[r];
+      }
+    }
+    f32x16 g;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) g[r] = p[r] * (dp[r] - dq_i);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * half + h;
+      const f16x8 gb = pack_p(g, h);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        acc[0][db] = mfma32(load_v_frag<D>(kv_t, j, db, lane), gb, acc[0][db]);
+    }
+  };
+
   const int kv_end = CAUSAL ? min(N, q0 + kBlk) : N;
   const int n_kt = (kv_end + kBQ - 1) / kBQ;
+  // rows past N (last block only) and, causal, keys after the wave's first query
+  const bool rows_edge = q0 + 32 * qw + 32 > N;
   issue(0, 0);
   wait_vmem();
   __syncthreads();
   for (int t = 0; t < n_kt; ++t) {
     const int st = t & 1;
-    if (t + 1 < n_kt) issue(t + 1, st ^ 1);
-    const char* kk_t = smem + st * STAGE;
-    const char* kv_t = kk_t + TILE;
-    const char* vk_t = kk_t + 2 * TILE;
+    const char* kt = smem + st * STAGE;
     const int kt0 = t * kBQ;
+    auto prefetch = [&] {
+      if (t + 1 < n_kt) issue(t + 1, st ^ 1);
+    };
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      // S^T and dP^T for 32 keys x this wave's 32 queries; register r holds
-      // key kt0 + 32 half + 8 (r/4) + 4 hi + r%4, lane l query l%32.
-      f32x16 s = {}, dp = {};
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
-        s = mfma32(load_k_frag<D>(kk_t, half, kk, lane), qf[kk], s);
-        dp = mfma32(load_k_frag<D>(vk_t, half, kk, lane), gf[kk], dp);
-      }
-      f32x16 g;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kidx = kt0 + 32 * half + 8 * (r >> 2) + 4 * hi + (r & 3);
-        float pv = exp2_hw(fmaf(s[r], c, -lq));
-        const bool dead = (kidx >= N) || (CAUSAL && kidx > query) || !row_ok;
-        pv = dead ? 0.f : pv;
-        g[r] = pv * (dp[r] - dq_i);
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int j = 2 * half + h;
-        const f16x8 gb = pack_p(g, h);
-#pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] = mfma32(load_v_frag<D>(kv_t, j, db, lane), gb, acc[db]);
-      }
+    for (int i = 0; i < 2 / G; ++i) {
+      const int half = G == 2 ? grp : i;
+      const bool edge = rows_edge || (kt0 + 32 * half + 32 > N) ||
+                        (CAUSAL && kt0 + 32 * half + 31 > q0 + 32 * qw);
+      if (i == 0) body(kt, kt0, half, edge, prefetch);
+      else body(kt, kt0, half, edge, [] {});
     }
     wait_vmem();
     __syncthreads();
   }
-  store_transposed<D>(dQ + head, N, q0 + 32 * wave, lane, acc, scale);
+  if constexpr (G == 2) group_reduce<1, DB>(smem, grp, qw, lane, acc);
+  if (grp == 0) store_transposed<D>(dQ + head, N, q0 + 32 * qw, lane, acc[0], scale);
 }
+
+// Wave groups per workgroup: two where the registers allow two waves per SIMD
+// (the second group takes the other half of every tile, so the grid stays
+// one workgroup per 128 rows and the SIMDs get a second wave to overlap).
+template <int D>
+constexpr int kDkdvGroups = D == 64 ? 2 : 1;
+template <int D>
+constexpr int kDqGroups = 2;
 
 template <int D, bool CAUSAL>
 static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
-                             float* di, int64_t BH, int N, hipStream_t s) {
+                             float* ws, int64_t BH, int N, hipStream_t s) {
   const float scale = (float)(1.0 / sqrt((double)D));
   const float c = scale * kLog2e;
   const f16* Q = (const f16*)q;
@@ -410,14 +507,17 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const f16* O = (const f16*)o;
   const f16* G = (const f16*)dout;
   const int64_t rows = BH * N;
+  float* di = ws;
+  float* nl = ws + rows;
   hipLaunchKernelGGL((fa_bwd_di_kernel<D>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, O,
-                     G, di, rows);
+                     G, lse, di, nl, rows);
   const int nb = (N + kBlk - 1) / kBlk;
   const int total = (int)(BH * nb);
-  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL>), dim3(total), dim3(256), 0, s, Q, K, V, G, lse,
-                     di, dk, dv, N, nb, total, c, scale);
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL>), dim3(total), dim3(256), 0, s, Q, K, V, G, lse,
-                     di, dq, N, nb, total, c, scale);
+  constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
+  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK>), dim3(total), dim3(256 * GK), 0, s, Q, K,
+                     V, G, nl, di, dk, dv, N, nb, total, c, scale);
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
+                     G, nl, di, dq, N, nb, total, c, scale);
   return hipGetLastError();
 }
 
@@ -426,7 +526,7 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
 
 extern "C" int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N) {
   if (B <= 0 || H <= 0 || N <= 0) return 0;
-  return B * H * N;
+  return 2 * B * H * N;   // D_i, then -L log2(e)
 }
 
 extern "C" int fa_bwd_f16(const void* q, const void* k, const void* v, const void* o,

@@ -84,7 +84,7 @@ int fa_validate_bwd(const void* q, const void* k, const void* v, const void* o,
                     const float* dv, const float* workspace, int64_t B, int64_t H,
                     int64_t N, int64_t D);
 
-/* Floats of the workspace fa_bwd_f16 needs: B*H*N (the row sums D_i). */
+/* Floats of the workspace fa_bwd_f16 needs: 2*B*H*N (the row sums D_i, then -lse*log2(e)). */
 int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N);
 
 /*
@@ -93,7 +93,7 @@ int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N);
  * forward's natural-log logsumexp), writes fp32 [B,H,N,D] gradients
  *   dq = dS k / sqrt(D),  dk = dS^T q / sqrt(D),  dv = P^T dout,
  * with P = exp(q k^T / sqrt(D) - lse) [causal-masked], dS = P * (dout v^T - D_i),
- * D_i = rowsum(dout * o). workspace: caller-provided fp32 [B*H*N].
+ * D_i = rowsum(dout * o). workspace: caller-provided fp32 [2*B*H*N].
  * Replaces flash_attn_backward (cuda/flash_attn_kernel.cu:417-503), which
  * takes the same six tensors (fp32 there) and returns [dQ, dK, dV]; the causal
  * flag and D = 128 have no reference counterpart.

@@ -147,7 +147,7 @@ def test_bwd_rejects_before_touching_the_device(capi):
     lib = capi.load()
     assert lib.fa_bwd_f16(*_bwd(D=80), 0, None) == capi.STATUS["FA_ERR_HEAD_DIM"]
     assert lib.fa_bwd_f16(*_bwd(ws=0), 1, None) == capi.STATUS["FA_ERR_NULL_POINTER"]
-    assert lib.fa_bwd_workspace_floats(2, 8, 4096) == 2 * 8 * 4096
+    assert lib.fa_bwd_workspace_floats(2, 8, 4096) == 2 * 2 * 8 * 4096
     assert lib.fa_bwd_workspace_floats(0, 8, 4096) == 0
 
 
