@@ -1,7 +1,7 @@
 """Benchmark: FlashAttention forward TFLOP/s (and % of dense FP16 MFMA peak) at
 B=1 H=8 N=4096 D=64 on one MI355X, plus the split-KV paged decode in GB/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|copy]
 
 A step is one ``forward(Q, K, V)`` call (O fp16 + L fp32) of the headline
 configuration (N=4096) on inputs resident in HBM.
@@ -142,6 +142,105 @@ def bench_backward(fa, torch, dev, reps=5, iters=20):
     return res
 
 
+def bench_pages(fa, torch, dev, reps=5, iters=20):
+    """KV page writer: a config-3-sized prefill reshaped into pages (HBM-bound
+    copy: K and V read once and written once) and a one-token decode append."""
+    res = {}
+    B, H, N, D = 4, 16, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(11)
+    k = torch.randn(B, H, N, D, device=dev, generator=g).half()
+    v = torch.randn(B, H, N, D, device=dev, generator=g).half()
+    pages = N // 16
+    table = torch.randperm(B * pages, device=dev, generator=g).to(torch.int32).view(B, pages)
+    kp = torch.empty(B * pages, H, 16, D, dtype=torch.half, device=dev)
+    vp = torch.empty_like(kp)
+    zero = torch.zeros(B, dtype=torch.int32, device=dev)
+    ms = median_of(lambda: fa.kv_append(k, v, kp, vp, table, zero), reps, 3, iters, torch)
+    nbytes = 2 * 2 * B * H * N * D * 2
+    res["prefill_B4H16N4096D128"] = {"ms": round(ms, 4), "GBps": round(nbytes / ms / 1e6, 1),
+                                     "pct_hbm": round(100 * nbytes / ms / 1e6 / PEAK_HBM_GBS, 1),
+                                     "bytes": nbytes}
+    del k, v, kp, vp
+    B, H, D, ctx = 32, 32, 128, 4000
+    pages = (ctx + 1 + 15) // 16
+    table = torch.randperm(B * pages, device=dev, generator=g).to(torch.int32).view(B, pages)
+    kp = torch.empty(B * pages, H, 16, D, dtype=torch.half, device=dev)
+    vp = torch.empty_like(kp)
+    kn = torch.randn(B, H, 1, D, device=dev, generator=g).half()
+    vn = torch.randn(B, H, 1, D, device=dev, generator=g).half()
+    pos = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    ms = median_of(lambda: fa.kv_append(kn, vn, kp, vp, table, pos), reps, 3, 100, torch)
+    res["decode_append_B32H32D128"] = {"us": round(ms * 1000, 2)}
+    return res
+
+
+def bench_sdpa(fa, torch, dev, reps=10):
+    """Paired comparison with PyTorch-ROCm's SDPA, the reference's headline
+    protocol (bench/bench_fa3_headline.py:1-91): clock burn-in, then per N ten
+    reps of both sides back to back in alternating order, the gap taken per
+    rep and the median reported. Ours is forward() (O and L), as there.
+    Timing only: SDPA's output is compared for information, not as parity."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    B, H, D = 1, 8, 64
+    qb = torch.randn(B, H, 4096, D, device=dev, dtype=torch.float16)
+    for _ in range(100):
+        fa.forward_only(qb, qb, qb)
+    torch.cuda.synchronize()
+    res = {}
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel(backend):
+                F.scaled_dot_product_attention(qb[:, :, :64], qb[:, :, :64], qb[:, :, :64])
+            torch.cuda.synchronize()
+            res["sdpa_backend"] = backend.name
+            break
+        except RuntimeError as e:   # backend not built into this torch
+            res.setdefault("unavailable", []).append(f"{backend.name}: {str(e)[:80]}")
+    if "sdpa_backend" not in res:
+        return res
+    be = getattr(SDPBackend, res["sdpa_backend"])
+
+    def med(xs):
+        xs = sorted(xs)
+        n = len(xs)
+        return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+    for N in (1024, 2048, 4096):
+        g = torch.Generator(device=dev).manual_seed(N)
+        Q, K, V = (torch.randn(B, H, N, D, device=dev, dtype=torch.float16, generator=g)
+                   for _ in range(3))
+        iters = 200 if N <= 1024 else (100 if N <= 2048 else 50)
+
+        def ours():
+            return time_events(lambda: fa.forward(Q, K, V), 30, iters, torch)
+
+        def sdpa():
+            with sdpa_kernel(be):
+                return time_events(lambda: F.scaled_dot_product_attention(Q, K, V), 30, iters, torch)
+
+        t_o, t_s, gaps = [], [], []
+        for r in range(reps):
+            if r % 2 == 0:
+                o = ours(); s_ = sdpa()
+            else:
+                s_ = sdpa(); o = ours()
+            t_o.append(o)
+            t_s.append(s_)
+            gaps.append((o / s_ - 1.0) * 100.0)
+        with sdpa_kernel(be):
+            Os = F.scaled_dot_product_attention(Q, K, V)
+        diff = float((fa.forward(Q, K, V)[0].float() - Os.float()).abs().max())
+        f = fwd_flops(B, H, N, D)
+        res[f"N{N}"] = {"ours_ms": round(med(t_o), 5), "sdpa_ms": round(med(t_s), 5),
+                        "ours_TFLOPs": round(f / med(t_o) / 1e9, 1),
+                        "sdpa_TFLOPs": round(f / med(t_s) / 1e9, 1),
+                        "paired_median_gap_pct": round(med(gaps), 2),
+                        "max_abs_diff_O": diff}
+    return res
+
+
 def cpu_baseline(budget_s=20.0):
     """Numpy oracle on the headline workload, bounded: whole heads until ~budget_s."""
     import numpy as np
@@ -205,7 +304,8 @@ def main():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "pages", "sdpa", "copy"],
+                    default="all")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -229,6 +329,12 @@ def main():
         return
     if args.only == "bwd":
         print(json.dumps({"backward": bench_backward(fa, torch, dev)}))
+        return
+    if args.only == "pages":
+        print(json.dumps({"kv_append": bench_pages(fa, torch, dev)}))
+        return
+    if args.only == "sdpa":
+        print(json.dumps({"sdpa_comparator": bench_sdpa(fa, torch, dev)}))
         return
 
     B, H, N, D = 1, 8, 4096, 64
@@ -301,6 +407,8 @@ def main():
         out["extra"] = extra
         out["decode"] = bench_decode(fa, torch, dev)
         out["backward"] = bench_backward(fa, torch, dev)
+        out["kv_append"] = bench_pages(fa, torch, dev)
+        out["sdpa_comparator"] = bench_sdpa(fa, torch, dev)
         out["copy_calibration"] = copy_calibration(torch, dev)
     if not args.no_cpu and args.only == "all":
         out["cpu_baseline"] = cpu_baseline(args.cpu_budget)

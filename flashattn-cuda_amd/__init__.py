@@ -13,6 +13,7 @@ reference's first module (cuda/flash_attn_kernel.cu:417-503):
 
 New entry points:
 
+    bad = kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos)   # in place
     O, L = decode_paged(q, k_pool, v_pool, page_table, ctx_lens, num_splits=16)
     part_o, part_lse = decode_partials(...);  O, L = lse_combine(part_o, part_lse)
 
@@ -67,6 +68,15 @@ def backward(Q, K, V, O, dO, L, causal: bool = False):
     The reference's backward(Q, K, V, O, dO, L) (cuda/flash_attn_kernel.cu:417-503).
     """
     return _C.backward(Q, K, V, O, dO, L, causal)
+
+
+def kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens=None):
+    """Write k_new/v_new [B,H,T,D] into the pools at start_pos[b] + t, in place.
+
+    Returns bad int32 [B]: 1 where a token of the sequence had no valid page
+    (that token is not written).
+    """
+    return _C.kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens)
 
 
 def decode_paged(q, k_pool, v_pool, page_table, ctx_lens, num_splits: int = 16):

@@ -30,7 +30,7 @@ EXT_NAME = "_fa_torch"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-HIP_SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_decode.hip", "fa_probe.hip"]
+HIP_SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_decode.hip", "fa_pages.hip", "fa_probe.hip"]
 CPP_SOURCES = ["fa_capi.cpp"]
 
 HIP_FLAGS = [

@@ -79,6 +79,8 @@ extern "C" int fa_validate_bwd(const void* q, const void* k, const void* v, cons
   return FA_OK;
 }
 
+// Decode arguments (no reference counterpart): pool/page-table shapes, the
+// split count and the grid limits of the split pass.
 extern "C" int fa_validate_decode(const void* q, const void* k_pool, const void* v_pool,
                                   const int32_t* page_table, const int32_t* ctx_lens,
                                   int64_t B, int64_t H, int64_t D, int64_t page_size,
@@ -97,6 +99,33 @@ extern "C" int fa_validate_decode(const void* q, const void* k_pool, const void*
   if (H > 65535 || B > 65535) return FA_ERR_TOO_LARGE;
   if (B > kMaxHeadElems / max_pages) return FA_ERR_TOO_LARGE;
   if (max_pages > kMaxHeadElems / page_size) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+// KV page writer arguments (no reference counterpart). T = 0 is a valid
+// no-op; grid is (ceil(T / rows), H, B).
+extern "C" int fa_validate_kv_append(const void* k_new, const void* v_new,
+                                     const int32_t* page_table, const int32_t* start_pos,
+                                     const int32_t* new_lens, const void* k_pool,
+                                     const void* v_pool, const int32_t* bad, int64_t B, int64_t H,
+                                     int64_t T, int64_t D, int64_t page_size, int64_t max_pages,
+                                     int64_t num_pages) {
+  // k_new/v_new may be NULL when there is nothing to copy (T = 0: an empty
+  // tensor has no storage).
+  if ((T != 0 && (!k_new || !v_new)) || !page_table || !start_pos || !k_pool || !v_pool)
+    return FA_ERR_NULL_POINTER;
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (T < 0) return FA_ERR_SEQ_LEN;
+  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
+  if (page_size != 16) return FA_ERR_PAGE_SIZE;
+  if (max_pages <= 0) return FA_ERR_MAX_PAGES;
+  if (num_pages <= 0) return FA_ERR_NUM_PAGES;
+  if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(k_pool) || !aligned16(v_pool))
+    return FA_ERR_ALIGNMENT;
+  const auto a4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; };
+  if (!a4(page_table) || !a4(start_pos) || !a4(new_lens) || !a4(bad)) return FA_ERR_ALIGNMENT;
+  if (H > 65535 || B > 65535) return FA_ERR_TOO_LARGE;
+  if (T > kMaxGrid || max_pages > kMaxGrid || num_pages > kMaxGrid) return FA_ERR_TOO_LARGE;
   return FA_OK;
 }
 

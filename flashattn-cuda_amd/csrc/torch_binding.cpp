@@ -232,6 +232,59 @@ std::vector<torch::Tensor> decode_paged(torch::Tensor q, torch::Tensor k_pool, t
   return {o, lse};
 }
 
+// kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens=None)
+// writes new rows into the pools in place and returns bad int32 [B] (1 where
+// a token of the sequence had no valid page). No reference counterpart.
+torch::Tensor kv_append(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_pool,
+                        torch::Tensor v_pool, torch::Tensor page_table, torch::Tensor start_pos,
+                        c10::optional<torch::Tensor> new_lens) {
+  TORCH_CHECK(k_new.is_cuda() && v_new.is_cuda() && k_pool.is_cuda() && v_pool.is_cuda() &&
+                  page_table.is_cuda() && start_pos.is_cuda(),
+              "k_new/v_new/k_pool/v_pool/page_table/start_pos must be CUDA tensors");
+  TORCH_CHECK(k_new.dim() == 4 && v_new.sizes() == k_new.sizes(),
+              "k_new and v_new must be [B, H, T, D] of the same shape");
+  TORCH_CHECK(k_pool.dim() == 4 && v_pool.sizes() == k_pool.sizes(),
+              "k_pool and v_pool must be [num_pages, H, page_size, D] of the same shape");
+  TORCH_CHECK(k_new.scalar_type() == torch::kHalf && v_new.scalar_type() == torch::kHalf &&
+                  k_pool.scalar_type() == torch::kHalf && v_pool.scalar_type() == torch::kHalf,
+              "k_new/v_new/k_pool/v_pool must be float16");
+  const int64_t B = k_new.size(0), H = k_new.size(1), T = k_new.size(2), D = k_new.size(3);
+  TORCH_CHECK(k_pool.size(1) == H && k_pool.size(3) == D,
+              "k_pool must be [num_pages, H, page_size, D] with k_new's H and D");
+  TORCH_CHECK(page_table.dim() == 2 && page_table.scalar_type() == torch::kInt &&
+                  page_table.size(0) == B,
+              "page_table must be int32 [B, max_pages]");
+  TORCH_CHECK(start_pos.dim() == 1 && start_pos.scalar_type() == torch::kInt &&
+                  start_pos.size(0) == B,
+              "start_pos must be int32 [B]");
+  const int32_t* lens = nullptr;
+  torch::Tensor nl;
+  if (new_lens.has_value()) {
+    nl = new_lens.value();
+    TORCH_CHECK(nl.is_cuda() && nl.dim() == 1 && nl.scalar_type() == torch::kInt &&
+                    nl.size(0) == B && nl.is_contiguous(),
+                "new_lens must be a contiguous CUDA int32 [B]");
+    lens = nl.data_ptr<int32_t>();
+  }
+  TORCH_CHECK(k_new.is_contiguous() && v_new.is_contiguous() && k_pool.is_contiguous() &&
+                  v_pool.is_contiguous() && page_table.is_contiguous() && start_pos.is_contiguous(),
+              "kv_append tensors must be contiguous");
+  const auto dev = k_new.device();
+  TORCH_CHECK(v_new.device() == dev && k_pool.device() == dev && v_pool.device() == dev &&
+                  page_table.device() == dev && start_pos.device() == dev &&
+                  (!nl.defined() || nl.device() == dev),
+              "kv_append tensors must be on the same device");
+  const c10::DeviceGuard guard(dev);
+  auto bad = torch::zeros({B}, page_table.options());
+  const int st = fa_kv_append_f16(k_new.data_ptr(), v_new.data_ptr(),
+                                  page_table.data_ptr<int32_t>(), start_pos.data_ptr<int32_t>(),
+                                  lens, k_pool.data_ptr(), v_pool.data_ptr(),
+                                  bad.data_ptr<int32_t>(), B, H, T, D, k_pool.size(2),
+                                  page_table.size(1), k_pool.size(0), current_stream(k_new));
+  check_status(st, "fa_kv_append_f16");
+  return bad;
+}
+
 // ---- layout probes (test support) ----
 torch::Tensor probe_mfma32(torch::Tensor a, torch::Tensor b, int64_t variant) {
   TORCH_CHECK(a.is_cuda() && a.sizes() == torch::IntArrayRef({32, 16}) && a.scalar_type() == torch::kHalf);
@@ -305,6 +358,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("backward", &backward, "FlashAttention backward: returns [dQ, dK, dV] float",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("dO"), py::arg("L"),
         py::arg("causal") = false);
+  m.def("kv_append", &kv_append, "write new K/V rows into the paged pools; returns bad [B]",
+        py::arg("k_new"), py::arg("v_new"), py::arg("k_pool"), py::arg("v_pool"),
+        py::arg("page_table"), py::arg("start_pos"), py::arg("new_lens") = py::none());
   m.def("decode_paged", &decode_paged, "split-KV paged decode: returns [O half, L float]",
         py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("page_table"),
         py::arg("ctx_lens"), py::arg("num_splits") = 16);

@@ -1,6 +1,6 @@
 /*
- * fa_mi355x.h — C ABI of the MI355X (gfx950) FlashAttention forward and the
- * split-KV paged decode.
+ * fa_mi355x.h — C ABI of the MI355X (gfx950) FlashAttention forward and
+ * backward, the split-KV paged decode and the KV-cache page writer.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t
  * passed as void*. The library never allocates, never synchronises the host
@@ -146,6 +146,35 @@ int fa_decode_paged_f16(const void* q, const void* k_pool, const void* v_pool,
                         int64_t max_pages, int64_t num_pages, int64_t num_splits,
                         float* part_o, float* part_lse, void* o, float* lse,
                         void* stream);
+
+/*
+ * Host-only argument check of fa_kv_append_f16. No reference counterpart.
+ */
+int fa_validate_kv_append(const void* k_new, const void* v_new, const int32_t* page_table,
+                          const int32_t* start_pos, const int32_t* new_lens, const void* k_pool,
+                          const void* v_pool, const int32_t* bad, int64_t B, int64_t H,
+                          int64_t T, int64_t D, int64_t page_size, int64_t max_pages,
+                          int64_t num_pages);
+
+/*
+ * KV-cache page writer (append, or reshape a prefill into pages): for each
+ * sequence b and new token t < n_b (n_b = new_lens[b] clamped to [0, T], or T
+ * if new_lens is NULL), copies k_new[b,h,t,:] and v_new[b,h,t,:] (fp16
+ * [B, H, T, D]) into k_pool / v_pool (fp16 [num_pages, H, 16, D], the layout
+ * fa_decode_paged_f16 reads) at position p = start_pos[b] + t: page
+ * page_table[b][p / 16], slot p % 16. Bit-exact copy. A token whose position
+ * is negative or not below max_pages*16, or whose page id is outside
+ * [0, num_pages), is not written; if `bad` is not NULL, bad[b] is set to 1
+ * for that sequence (the caller zeroes `bad`). With T = 0 nothing is copied
+ * and k_new / v_new may be NULL. Tokens of different sequences must not map
+ * to the same (page, slot): such writes race. No reference
+ * counterpart (the reference has no KV cache); it is the step before the
+ * paged decode.
+ */
+int fa_kv_append_f16(const void* k_new, const void* v_new, const int32_t* page_table,
+                     const int32_t* start_pos, const int32_t* new_lens, void* k_pool,
+                     void* v_pool, int32_t* bad, int64_t B, int64_t H, int64_t T, int64_t D,
+                     int64_t page_size, int64_t max_pages, int64_t num_pages, void* stream);
 
 #ifdef __cplusplus
 }

@@ -33,6 +33,10 @@ Pinning status (each function is checked in tests/test_oracle.py):
   over the contiguous keys; gather equals a direct index walk.
 * split_partials + lse_combine: combine of any split count equals the
   unsplit result; one split is the identity; empty splits carry weight 0.
+* append_pages: appending a prefill into an empty pool and reading it back
+  with gather_pages returns the rows (gather_pages is itself pinned by an
+  explicit index walk); appending in two steps equals one step; invalid page
+  ids and positions write nothing and set the flag.
 * naive_attention_backward (tests/test_backward.py:20-46): float64 central
   finite differences of sum(naive_attention(Q, K, V) * dO) in every input
   element, causal and not, on tiny inputs.
@@ -185,6 +189,38 @@ def gather_pages(pool, page_table, ctx_len: int, b: int, h: int):
     ids = np.asarray(page_table[b, :n_pages], dtype=np.int64)
     rows = pool[ids, h]                          # [n_pages, page_size, D]
     return rows.reshape(n_pages * page_size, pool.shape[3])[:ctx_len]
+
+
+def append_pages(k_pool, v_pool, page_table, start_pos, k_new, v_new, new_lens=None):
+    """Pools after writing k_new/v_new [B, H, T, D] at positions start_pos[b] + t.
+
+    Position p of sequence b is slot p % page_size of page page_table[b][p //
+    page_size] (the layout ``gather_pages`` reads). Sequence b writes its first
+    new_lens[b] tokens (clamped to [0, T]; all T if new_lens is None). A token
+    with a negative position, a position past the table, or a page id outside
+    [0, num_pages) is skipped and flags bad[b] = 1. Returns (k_pool', v_pool',
+    bad) on copies; no reference counterpart (the reference has no KV cache).
+    """
+    kp = np.array(k_pool, copy=True)
+    vp = np.array(v_pool, copy=True)
+    num_pages, _, page_size, _ = kp.shape
+    B, H, T, _ = k_new.shape
+    max_pages = page_table.shape[1]
+    bad = np.zeros(B, dtype=np.int32)
+    for b in range(B):
+        n = T if new_lens is None else min(max(int(new_lens[b]), 0), T)
+        for t in range(n):
+            p = int(start_pos[b]) + t
+            if p < 0 or p >= max_pages * page_size:
+                bad[b] = 1
+                continue
+            pid = int(page_table[b, p // page_size])
+            if pid < 0 or pid >= num_pages:
+                bad[b] = 1
+                continue
+            kp[pid, :, p % page_size] = k_new[b, :, t]
+            vp[pid, :, p % page_size] = v_new[b, :, t]
+    return kp, vp, bad
 
 
 def decode_attention(q, k_pool, v_pool, page_table, ctx_lens, dtype=np.float32):

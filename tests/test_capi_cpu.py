@@ -157,3 +157,40 @@ def test_torch_backward_checks_mirror_reference(fa):
     x = torch.zeros(1, 1, 8, 64)
     with pytest.raises(RuntimeError, match="Q must be a CUDA tensor"):
         fa.backward(x, x, x, x, x, torch.zeros(1, 1, 8))
+
+
+def _kv(**kw):
+    b = dict(kn=A, vn=A, pt=A, st=A, nl=None, kp=A, vp=A, bad=None, B=32, H=8, T=1, D=128, ps=16,
+             maxp=2048, np_=65536)
+    b.update(kw)
+    return tuple(b[k] for k in ("kn", "vn", "pt", "st", "nl", "kp", "vp", "bad", "B", "H", "T",
+                                "D", "ps", "maxp", "np_"))
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), "FA_OK"),
+    (dict(T=0), "FA_OK"),
+    (dict(T=0, kn=0, vn=0), "FA_OK"),
+    (dict(T=1, kn=0), "FA_ERR_NULL_POINTER"),
+    (dict(nl=A, bad=A, T=4096, D=64), "FA_OK"),
+    (dict(T=-1), "FA_ERR_SEQ_LEN"),
+    (dict(kp=0), "FA_ERR_NULL_POINTER"),
+    (dict(st=0), "FA_ERR_NULL_POINTER"),
+    (dict(D=96), "FA_ERR_HEAD_DIM"),
+    (dict(B=0), "FA_ERR_BATCH_HEADS"),
+    (dict(ps=32), "FA_ERR_PAGE_SIZE"),
+    (dict(maxp=0), "FA_ERR_MAX_PAGES"),
+    (dict(np_=0), "FA_ERR_NUM_PAGES"),
+    (dict(vn=A + 8), "FA_ERR_ALIGNMENT"),
+    (dict(nl=A + 2), "FA_ERR_ALIGNMENT"),
+    (dict(H=70000), "FA_ERR_TOO_LARGE"),
+])
+def test_validate_kv_append(capi, kw, code):
+    lib = capi.load()
+    assert lib.fa_validate_kv_append(*_kv(**kw)) == capi.STATUS[code]
+
+
+def test_kv_append_rejects_before_touching_the_device(capi):
+    lib = capi.load()
+    assert lib.fa_kv_append_f16(*_kv(ps=8), None) == capi.STATUS["FA_ERR_PAGE_SIZE"]
+    assert lib.fa_kv_append_f16(*_kv(T=0), None) == capi.STATUS["FA_OK"]   # no launch

@@ -389,3 +389,86 @@ def test_planted_backward_mistakes_are_caught(mut):
         if not all(np.allclose(g, r, atol=1e-6, rtol=1e-6) for g, r in zip(got, ref)):
             return
     pytest.fail("finite differences did not catch the planted mistake")
+
+
+# ---------------------------------------------------------------- page writer
+def _pool_case(seed=3, B=3, H=2, D=8, T=37, page_size=16):
+    rng = np.random.default_rng(seed)
+    max_pages = (T + 40 + page_size - 1) // page_size + 1
+    num_pages = B * max_pages + 5
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = perm[:B * max_pages].reshape(B, max_pages)
+    kp = rng.standard_normal((num_pages, H, page_size, D)).astype(np.float16)
+    vp = rng.standard_normal((num_pages, H, page_size, D)).astype(np.float16)
+    kn = rng.standard_normal((B, H, T, D)).astype(np.float16)
+    vn = rng.standard_normal((B, H, T, D)).astype(np.float16)
+    return kp, vp, table, kn, vn
+
+
+def test_append_then_gather_returns_rows():
+    kp, vp, table, kn, vn = _pool_case()
+    B, H, T, _ = kn.shape
+    kp2, vp2, bad = orc.append_pages(kp, vp, table, np.zeros(B, np.int32), kn, vn)
+    assert not bad.any()
+    for b in range(B):
+        for h in range(H):
+            np.testing.assert_array_equal(orc.gather_pages(kp2, table, T, b, h), kn[b, h])
+            np.testing.assert_array_equal(orc.gather_pages(vp2, table, T, b, h), vn[b, h])
+    # pages not in any sequence's first ceil(T/16) entries are untouched
+    used = set(table[:, : (T + 15) // 16].ravel().tolist())
+    for pid in range(kp.shape[0]):
+        if pid not in used:
+            np.testing.assert_array_equal(kp2[pid], kp[pid])
+
+
+def test_append_in_two_steps_equals_one():
+    kp, vp, table, kn, vn = _pool_case(seed=4)
+    B, H, T, _ = kn.shape
+    start = np.array([0, 5, 17], np.int32)
+    one = orc.append_pages(kp, vp, table, start, kn, vn)
+    cut = 13
+    a = orc.append_pages(kp, vp, table, start, kn[:, :, :cut], vn[:, :, :cut])
+    two = orc.append_pages(a[0], a[1], table, start + cut, kn[:, :, cut:], vn[:, :, cut:])
+    np.testing.assert_array_equal(one[0], two[0])
+    np.testing.assert_array_equal(one[1], two[1])
+    # ragged counts: writing n_b tokens equals writing the truncated batch row by row
+    lens = np.array([0, 9, 37], np.int32)
+    r = orc.append_pages(kp, vp, table, start, kn, vn, lens)
+    for b in range(B):
+        rb = orc.append_pages(kp, vp, table[b:b + 1], start[b:b + 1], kn[b:b + 1, :, :lens[b]],
+                              vn[b:b + 1, :, :lens[b]])
+        used = table[b, start[b] // 16:(start[b] + max(lens[b], 1) + 15) // 16 + 1]
+        for pid in used:
+            np.testing.assert_array_equal(r[0][pid], rb[0][pid])
+
+
+def test_append_invalid_pages_write_nothing():
+    kp, vp, table, kn, vn = _pool_case(seed=5)
+    B = kn.shape[0]
+    bad_table = table.copy()
+    bad_table[1, 0] = -1                      # sequence 1's first page invalid
+    bad_table[2, 1] = kp.shape[0]             # sequence 2's second page past the pool
+    start = np.array([0, 0, 0], np.int32)
+    kp2, vp2, bad = orc.append_pages(kp, vp, bad_table, start, kn, vn)
+    assert bad.tolist() == [0, 1, 1]
+    # past the table: positions beyond max_pages * 16
+    far = np.array([bad_table.shape[1] * 16 - 3, -1, 0], np.int32)
+    _, _, bad2 = orc.append_pages(kp, vp, table, far, kn[:, :, :5], vn[:, :, :5])
+    assert bad2.tolist() == [1, 1, 0]
+
+
+@pytest.mark.parametrize("mistake", ["slot_from_page", "head_stride"])
+def test_planted_append_mistakes_are_caught(mistake):
+    kp, vp, table, kn, vn = _pool_case(seed=6)
+    B, H, T, D = kn.shape
+    bad_kp = np.array(kp, copy=True)
+    for b in range(B):
+        for t in range(T):
+            pid = table[b, t // 16]
+            if mistake == "slot_from_page":   # slot and page index swapped
+                bad_kp[table[b, t % 16 if t % 16 < table.shape[1] else 0], :, t // 16] = kn[b, :, t]
+            else:                             # heads written in reverse order
+                bad_kp[pid, ::-1, t % 16] = kn[b, :, t]
+    ok = all(np.array_equal(orc.gather_pages(bad_kp, table, T, b, h), kn[b, h])
+             for b in range(B) for h in range(H))
+    assert not ok
