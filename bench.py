@@ -109,6 +109,14 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
     other = float(pages.sum() * 4 + B * H * D * 2 * 2 + B * H * 4)
     alg = kv_bytes + other
     del kp, vp
+    # GQA: the same contexts with 8 KV heads shared by groups of 4 query heads.
+    # Bytes count each KV page once (what a group-aware kernel must read).
+    Hkv = 8
+    kp = torch.randn(P, Hkv, 16, D, device=dev, dtype=torch.float16, generator=g)
+    vp = torch.randn(P, Hkv, 16, D, device=dev, dtype=torch.float16, generator=g)
+    ms_gqa = median_of(lambda: fa.decode_paged(q, kp, vp, tt, tc, S), reps, 3, iters, torch)
+    alg_gqa = kv_bytes * Hkv / H + other
+    del kp, vp
     torch.cuda.empty_cache()
     return {
         "workload": "decode B32 H32 D128 ctx~U[512,32768] seed5, 16-token pages, 16 splits",
@@ -117,6 +125,8 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
         "GBps": round(alg / (ms * 1e-3) / 1e9, 1),
         "pct_hbm_peak": round(100 * alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
         "split_pass_GBps": round(alg / (ms_split * 1e-3) / 1e9, 1),
+        "gqa_H32_Hkv8": {"ms": round(ms_gqa, 5), "algorithmic_bytes": alg_gqa,
+                         "GBps_unique_kv": round(alg_gqa / (ms_gqa * 1e-3) / 1e9, 1)},
     }
 
 

@@ -6,7 +6,9 @@ Drop-in for the reference's torch-extension module
     O, L = forward(Q, K, V)           # O fp16 [B,H,N,D], L fp32 [B,H,N]
     O = forward_only(Q, K, V)         # bitwise the same O, no L
 
-Both accept ``causal=True`` and D in {64, 128}. The backward of the
+Both accept ``causal=True``, D in {64, 128} and K/V with fewer heads than Q
+(GQA/MQA: [B, H_kv, N, D], H a multiple of H_kv); ``forward_varlen`` takes
+packed variable-length sequences. The backward of the
 reference's first module (cuda/flash_attn_kernel.cu:417-503):
 
     dQ, dK, dV = backward(Q, K, V, O, dO, L)   # fp32 [B,H,N,D]
@@ -55,6 +57,15 @@ EXT_PATH = _EXT
 def forward(Q, K, V, causal: bool = False):
     """[O, L]: O = softmax(Q K^T / sqrt(D)) V (fp16), L = row logsumexp (fp32)."""
     return _C.forward(Q, K, V, causal)
+
+
+def forward_varlen(q, k, v, cu_seqlens, max_seqlen: int, causal: bool = False):
+    """[O, L] of B packed sequences, head-major: q [H, total, D], k/v [H_kv, total, D].
+
+    Sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1] (int32 [B+1]) of every
+    head and attends only within itself; max_seqlen must cover every sequence.
+    """
+    return _C.forward_varlen(q, k, v, cu_seqlens, max_seqlen, causal)
 
 
 def forward_only(Q, K, V, causal: bool = False):

@@ -38,6 +38,11 @@ SIGNATURES = {
     "fa_validate_bwd": (C.c_int, [_vp] * 10 + [_i64] * 4),
     "fa_bwd_workspace_floats": (_i64, [_i64, _i64, _i64]),
     "fa_bwd_f16": (C.c_int, [_vp] * 10 + [_i64] * 4 + [C.c_int, _vp]),
+    "fa_validate_fwd_gqa": (C.c_int, [_vp] * 4 + [_i64] * 5),
+    "fa_fwd_gqa_f16": (C.c_int, [_vp] * 5 + [_i64] * 5 + [C.c_int, _vp]),
+    "fa_validate_fwd_varlen": (C.c_int, [_vp] * 5 + [_i64] * 6),
+    "fa_fwd_varlen_f16": (C.c_int, [_vp] * 6 + [_i64] * 6 + [C.c_int, _vp]),
+    "fa_decode_paged_gqa_f16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 5),
     "fa_validate_kv_append": (C.c_int, [_vp] * 8 + [_i64] * 7),
     "fa_kv_append_f16": (C.c_int, [_vp] * 8 + [_i64] * 7 + [_vp]),
     "fa_probe_fwd_variant": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp]),
@@ -49,7 +54,7 @@ STATUS = {
     "FA_OK": 0, "FA_ERR_NULL_POINTER": 1, "FA_ERR_HEAD_DIM": 2, "FA_ERR_SEQ_LEN": 3,
     "FA_ERR_BATCH_HEADS": 4, "FA_ERR_ALIGNMENT": 5, "FA_ERR_TOO_LARGE": 6,
     "FA_ERR_PAGE_SIZE": 7, "FA_ERR_NUM_SPLITS": 8, "FA_ERR_MAX_PAGES": 9,
-    "FA_ERR_NUM_PAGES": 10,
+    "FA_ERR_NUM_PAGES": 10, "FA_ERR_KV_HEADS": 11,
 }
 
 

@@ -33,6 +33,7 @@ extern "C" const char* fa_status_str(int status) {
     case FA_ERR_NUM_SPLITS: return "num_splits must be in [1, 16]";
     case FA_ERR_MAX_PAGES: return "max_pages must be > 0";
     case FA_ERR_NUM_PAGES: return "num_pages must be > 0";
+    case FA_ERR_KV_HEADS: return "H must be a positive multiple of H_kv";
     default: break;
   }
   if (status < 0) return "HIP error (negated hipError_t)";
@@ -54,6 +55,35 @@ extern "C" int fa_validate_fwd(const void* q, const void* k, const void* v, cons
   const int64_t bh = B * H;
   const int64_t num_qb = (N + 127) / 128;
   if (bh > kMaxGrid / num_qb) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+// GQA: the dense checks plus the head grouping.
+extern "C" int fa_validate_fwd_gqa(const void* q, const void* k, const void* v, const void* o,
+                                   int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D) {
+  const int st = fa_validate_fwd(q, k, v, o, B, H, N, D);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  return FA_OK;
+}
+
+// Varlen: one head's packed rows are addressed with size_t offsets; one
+// sequence (at most max_seqlen rows) through a 32-bit buffer range.
+extern "C" int fa_validate_fwd_varlen(const void* q, const void* k, const void* v, const void* o,
+                                      const int32_t* cu_seqlens, int64_t B, int64_t H,
+                                      int64_t H_kv, int64_t max_seqlen, int64_t total,
+                                      int64_t D) {
+  if (!q || !k || !v || !o || !cu_seqlens) return FA_ERR_NULL_POINTER;
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (max_seqlen <= 0 || total < 0) return FA_ERR_SEQ_LEN;
+  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return FA_ERR_ALIGNMENT;
+  if (reinterpret_cast<uintptr_t>(cu_seqlens) & 3u) return FA_ERR_ALIGNMENT;
+  if (max_seqlen * D * 2 > kMaxHeadElems || total > kMaxGrid) return FA_ERR_TOO_LARGE;
+  if (B > kMaxGrid / H) return FA_ERR_TOO_LARGE;
+  const int64_t num_qb = (max_seqlen + 127) / 128;
+  if (B * H > kMaxGrid / num_qb) return FA_ERR_TOO_LARGE;
   return FA_OK;
 }
 

@@ -5,7 +5,8 @@
 // page table, computed per (sequence, head, split) as a normalised partial
 // (O_s, L_s), then merged by L = log sum_s exp(L_s), O = sum_s exp(L_s - L) O_s.
 //
-// Pool layout: [num_pages, H, 16, D] fp16, so the 16 tokens of one head in a
+// Pool layout: [num_pages, H_kv, 16, D] fp16 (H_kv = H, or fewer KV heads
+// shared by groups of H / H_kv query heads), so the 16 tokens of one head in a
 // page are 16*D*2 contiguous bytes (4 KiB at D=128): one wave reads a page of
 // one head as fully coalesced 16-byte loads.
 //
@@ -32,7 +33,7 @@ __global__ void __launch_bounds__(kDecThreads)
 fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
                        const f16* __restrict__ vpool, const int32_t* __restrict__ page_table,
                        const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
-                       float* __restrict__ part_lse, int H, int max_pages, int num_pages,
+                       float* __restrict__ part_lse, int H, int Hkv, int max_pages, int num_pages,
                        int S, float c) {
   constexpr int DPL = D / 4;   // d per lane
   constexpr int NV = DPL / 8;  // 16-byte vectors per lane per row
@@ -77,7 +78,8 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
   for (int p = p0 + wave; p < p1; p += kDecWaves) {
     const int pid = pt[p];
     if (pid < 0 || pid >= num_pages) { bad = true; continue; }
-    const size_t base = ((size_t)pid * H + h) * (kPage * D) + (size_t)tok * D + dq * DPL;
+    const size_t base = ((size_t)pid * Hkv + h / (H / Hkv)) * (kPage * D) + (size_t)tok * D +
+                        dq * DPL;
     f16x8 kv[NV], vv[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
@@ -189,15 +191,13 @@ fa_lse_combine_kernel(const float* __restrict__ part_o, const float* __restrict_
 
 }  // namespace fa
 
-extern "C" int fa_decode_split_f16(const void* q, const void* k_pool, const void* v_pool,
-                                   const int32_t* page_table, const int32_t* ctx_lens,
-                                   int64_t B, int64_t H, int64_t D, int64_t page_size,
-                                   int64_t max_pages, int64_t num_pages, int64_t num_splits,
-                                   float* part_o, float* part_lse, void* stream) {
-  using namespace fa;
-  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
-                              max_pages, num_pages, num_splits);
-  if (st != FA_OK) return st;
+namespace fa {
+// Split pass with query heads h reading pool head h / (H / Hkv); arguments
+// already validated.
+static int decode_split(const void* q, const void* k_pool, const void* v_pool,
+                        const int32_t* page_table, const int32_t* ctx_lens, int64_t B, int64_t H,
+                        int64_t Hkv, int64_t D, int64_t max_pages, int64_t num_pages,
+                        int64_t num_splits, float* part_o, float* part_lse, void* stream) {
   if (!part_o || !part_lse) return FA_ERR_NULL_POINTER;
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -205,16 +205,29 @@ extern "C" int fa_decode_split_f16(const void* q, const void* k_pool, const void
   if (D == 128) {
     hipLaunchKernelGGL((fa_decode_split_kernel<128>), grid, dim3(kDecThreads), 0, s,
                        (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table,
-                       ctx_lens, part_o, part_lse, (int)H, (int)max_pages, (int)num_pages,
-                       (int)num_splits, c);
+                       ctx_lens, part_o, part_lse, (int)H, (int)Hkv, (int)max_pages,
+                       (int)num_pages, (int)num_splits, c);
   } else {
     hipLaunchKernelGGL((fa_decode_split_kernel<64>), grid, dim3(kDecThreads), 0, s,
                        (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table,
-                       ctx_lens, part_o, part_lse, (int)H, (int)max_pages, (int)num_pages,
-                       (int)num_splits, c);
+                       ctx_lens, part_o, part_lse, (int)H, (int)Hkv, (int)max_pages,
+                       (int)num_pages, (int)num_splits, c);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? FA_OK : -(int)e;
+}
+}  // namespace fa
+
+extern "C" int fa_decode_split_f16(const void* q, const void* k_pool, const void* v_pool,
+                                   const int32_t* page_table, const int32_t* ctx_lens,
+                                   int64_t B, int64_t H, int64_t D, int64_t page_size,
+                                   int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                                   float* part_o, float* part_lse, void* stream) {
+  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
+                              max_pages, num_pages, num_splits);
+  if (st != FA_OK) return st;
+  return fa::decode_split(q, k_pool, v_pool, page_table, ctx_lens, B, H, H, D, max_pages,
+                          num_pages, num_splits, part_o, part_lse, stream);
 }
 
 extern "C" int fa_lse_combine_f32(const float* part_o, const float* part_lse, int64_t B,
@@ -246,6 +259,22 @@ extern "C" int fa_decode_paged_f16(const void* q, const void* k_pool, const void
                                    void* stream) {
   int st = fa_decode_split_f16(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
                                max_pages, num_pages, num_splits, part_o, part_lse, stream);
+  if (st != FA_OK) return st;
+  return fa_lse_combine_f32(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
+}
+
+extern "C" int fa_decode_paged_gqa_f16(const void* q, const void* k_pool, const void* v_pool,
+                                       const int32_t* page_table, const int32_t* ctx_lens,
+                                       int64_t B, int64_t H, int64_t H_kv, int64_t D,
+                                       int64_t page_size, int64_t max_pages, int64_t num_pages,
+                                       int64_t num_splits, float* part_o, float* part_lse,
+                                       void* o, float* lse, void* stream) {
+  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
+                              max_pages, num_pages, num_splits);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  st = fa::decode_split(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D, max_pages,
+                        num_pages, num_splits, part_o, part_lse, stream);
   if (st != FA_OK) return st;
   return fa_lse_combine_f32(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
 }

@@ -59,6 +59,47 @@ __device__ __forceinline__ int xcd_remap(int g, int total) {
   return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
+// Where the heads of one launch live. Dense: Q/O [B, H, N, D], K/V
+// [B, H/group, N, D], L [B, H, N]. Varlen (cu != nullptr): sequences packed
+// head-major, Q/O [H, total, D], K/V [H/group, total, D], L [H, total];
+// sequence b is rows cu[b] .. cu[b+1] of every head and N is the grid's
+// maximum length. Query head h reads KV head h / group (GQA / MQA).
+struct Geom {
+  const int32_t* cu;
+  int N;
+  int H;
+  int group;
+  int total;
+};
+
+// One (b, h): element offsets of its Q/O and K/V rows, of its L row, and its
+// length. Varlen bounds are clamped into [0, total] and to N, so a malformed
+// cu never moves a head's buffer range outside its own rows.
+struct HeadView {
+  size_t q, kv, l;
+  int n;
+};
+
+template <int D>
+__device__ __forceinline__ HeadView head_view(const Geom& g, int bh) {
+  HeadView v;
+  if (g.cu == nullptr) {
+    v.n = g.N;
+    v.q = (size_t)bh * g.N * D;
+    v.kv = (size_t)(bh / g.group) * g.N * D;
+    v.l = (size_t)bh * g.N;
+  } else {
+    const int b = bh / g.H, h = bh - b * g.H;
+    const int s0 = min(max(g.cu[b], 0), g.total);
+    const int s1 = min(max(g.cu[b + 1], s0), g.total);
+    v.n = min(s1 - s0, g.N);
+    v.q = ((size_t)h * g.total + s0) * D;
+    v.kv = ((size_t)(h / g.group) * g.total + s0) * D;
+    v.l = (size_t)h * g.total + s0;
+  }
+  return v;
+}
+
 // State and tile operations of one wave: 32 query rows, one lane pair per row
 // (lanes l and l^32 hold the two halves of every 32-key block).
 template <int D, bool CAUSAL, bool FULL>
@@ -323,7 +364,7 @@ template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
 __global__ void __launch_bounds__(256 * KSPLIT)
 fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                     const f16* __restrict__ V, f16* __restrict__ O,
-                    float* __restrict__ L, int N, int num_qb, int total, float c) {
+                    float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
   constexpr int TILE = kBC * D * 2;
   constexpr int BLOCKS = TILE / 1024;                     // 1 KiB blocks per tile
   constexpr int WAVES = kRowGroups * KSPLIT;
@@ -348,10 +389,13 @@ fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   int qb = logical - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
 
-  const size_t head = (size_t)bh * N * D;
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (qb * kBR >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
   const int head_bytes = N * D * 2;
-  const char* Kh = reinterpret_cast<const char*>(K + head);
-  const char* Vh = reinterpret_cast<const char*>(V + head);
+  const char* Kh = reinterpret_cast<const char*>(K + hv.kv);
+  const char* Vh = reinterpret_cast<const char*>(V + hv.kv);
   const int q0 = qb * kBR;
 
   RB rb;
@@ -450,7 +494,7 @@ fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int s2 = 1; s2 < KSPLIT; ++s2) rb.merge_from(area + (s2 - 1) * REC);
   }
-  rb.template finish<WRITE_L>(O + head, L + (size_t)bh * N);
+  rb.template finish<WRITE_L>(O + head, L + hv.l);
 }
 
 // f(integral_constant<int, I>) for I = B .. E-1, expanded at compile time
@@ -490,7 +534,7 @@ template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int RING>
 __global__ void __launch_bounds__(256 * KSPLIT)
 fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, f16* __restrict__ O,
-                   float* __restrict__ L, int N, int num_qb, int total, float c) {
+                   float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
   constexpr int TILE = kBC * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int WAVES = kRowGroups * KSPLIT;
@@ -523,10 +567,13 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   int qb = logical - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;
 
-  const size_t head = (size_t)bh * N * D;
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (qb * kBR >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
   const int head_bytes = N * D * 2;
-  const char* Kh = reinterpret_cast<const char*>(K + head);
-  const char* Vh = reinterpret_cast<const char*>(V + head);
+  const char* Kh = reinterpret_cast<const char*>(K + hv.kv);
+  const char* Vh = reinterpret_cast<const char*>(V + hv.kv);
   const int q0 = qb * kBR;
 
   RB rb;
@@ -740,7 +787,7 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int s2 = 1; s2 < KSPLIT; ++s2) rb.merge_from(area + (s2 - 1) * REC);
   }
-  rb.template finish<WRITE_L>(O + head, L + (size_t)bh * N);
+  rb.template finish<WRITE_L>(O + head, L + hv.l);
 }
 
 // ---------------------------------------------------------------------------
@@ -776,7 +823,7 @@ template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING>
 __global__ void __launch_bounds__(512)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
-                 float* __restrict__ L, int N, int num_qb, int total, float c) {
+                 float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
   static_assert(RING == 4 || RING == 6, "an even ring of four or six tiles");
   constexpr int TILE = kBC * D * 2;
   constexpr int BLOCKS = TILE / 1024;          // 1 KiB blocks per tile
@@ -803,10 +850,13 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   int qb = logical - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
 
-  const size_t head = (size_t)bh * N * D;
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (qb * kBR >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
   const int head_bytes = N * D * 2;
-  const char* Kh = reinterpret_cast<const char*>(K + head);
-  const char* Vh = reinterpret_cast<const char*>(V + head);
+  const char* Kh = reinterpret_cast<const char*>(K + hv.kv);
+  const char* Vh = reinterpret_cast<const char*>(V + hv.kv);
   const int q0 = qb * kBR;
 
   RB rb;
@@ -981,7 +1031,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   __syncthreads();
   if (grp == 1) return;
   rb.merge_from(area);
-  rb.template finish<WRITE_L>(O + head, L + (size_t)bh * N);
+  rb.template finish<WRITE_L>(O + head, L + hv.l);
 }
 
 // Kernel variants: 10*k + s = split kernel with KSPLIT k and s LDS stages;
@@ -991,17 +1041,17 @@ constexpr int kPingPong = 204;
 constexpr int pipe_code(int ksplit, int ring) { return 100 + 10 * ring + ksplit; }
 
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
-static void launch_split(const f16* Q, const f16* K, const f16* V, f16* O, float* L, int N,
+static void launch_split(const f16* Q, const f16* K, const f16* V, f16* O, float* L, Geom geo,
                          int num_qb, int total, float c, hipStream_t stream) {
   hipLaunchKernelGGL((fa_fwd_split_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, STAGES>), dim3(total),
-                     dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, N, num_qb, total, c);
+                     dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, geo, num_qb, total, c);
 }
 
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int RING>
-static void launch_pipe(const f16* Q, const f16* K, const f16* V, f16* O, float* L, int N,
+static void launch_pipe(const f16* Q, const f16* K, const f16* V, f16* O, float* L, Geom geo,
                         int num_qb, int total, float c, hipStream_t stream) {
   hipLaunchKernelGGL((fa_fwd_pipe_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, RING>), dim3(total),
-                     dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, N, num_qb, total, c);
+                     dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, geo, num_qb, total, c);
 }
 
 // Variants that exist and whose LDS fits in 160 KiB.
@@ -1020,7 +1070,7 @@ static bool variant_fits(int D, int variant) {
 
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL>
 static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o,
-                             float* lse, int N, int num_qb, int total, float c, int variant,
+                             float* lse, Geom geo, int num_qb, int total, float c, int variant,
                              hipStream_t stream) {
   const f16* Q = (const f16*)q;
   const f16* K = (const f16*)k;
@@ -1029,29 +1079,29 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
   switch (variant) {
     case kPingPong:
       hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4>), dim3(total), dim3(512), 0,
-                         stream, Q, K, V, Op, lse, N, num_qb, total, c);
+                         stream, Q, K, V, Op, lse, geo, num_qb, total, c);
       break;
-    case pipe_code(1, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
-    case pipe_code(1, 3): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
-    case pipe_code(1, 4): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
-    case pipe_code(2, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 2, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
+    case pipe_code(1, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 2>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
+    case pipe_code(1, 3): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
+    case pipe_code(1, 4): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
+    case pipe_code(2, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 2, 2>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
     case pipe_code(2, 3):
-      if constexpr (D == 64) { launch_pipe<D, CAUSAL, WRITE_L, FULL, 2, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break; }
+      if constexpr (D == 64) { launch_pipe<D, CAUSAL, WRITE_L, FULL, 2, 3>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break; }
       return hipErrorInvalidValue;
-    case 13: launch_split<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
-    case 14: launch_split<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
-    case 22: launch_split<D, CAUSAL, WRITE_L, FULL, 2, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break;
+    case 13: launch_split<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
+    case 14: launch_split<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
+    case 22: launch_split<D, CAUSAL, WRITE_L, FULL, 2, 2>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
     case 23:
-      if constexpr (D == 64) { launch_split<D, CAUSAL, WRITE_L, FULL, 2, 3>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break; }
+      if constexpr (D == 64) { launch_split<D, CAUSAL, WRITE_L, FULL, 2, 3>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break; }
       return hipErrorInvalidValue;
     case 24:
-      if constexpr (D == 64) { launch_split<D, CAUSAL, WRITE_L, FULL, 2, 4>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break; }
+      if constexpr (D == 64) { launch_split<D, CAUSAL, WRITE_L, FULL, 2, 4>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break; }
       return hipErrorInvalidValue;
     case 42:
-      if constexpr (D == 64) { launch_split<D, CAUSAL, WRITE_L, FULL, 4, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream); break; }
+      if constexpr (D == 64) { launch_split<D, CAUSAL, WRITE_L, FULL, 4, 2>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break; }
       return hipErrorInvalidValue;
     default:
-      launch_split<D, CAUSAL, WRITE_L, FULL, 1, 2>(Q, K, V, Op, lse, N, num_qb, total, c, stream);
+      launch_split<D, CAUSAL, WRITE_L, FULL, 1, 2>(Q, K, V, Op, lse, geo, num_qb, total, c, stream);
       break;
   }
   return hipGetLastError();
@@ -1059,14 +1109,14 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
 
 template <int D, bool CAUSAL>
 static hipError_t dispatch_wl(const void* q, const void* k, const void* v, void* o,
-                              float* lse, int N, int num_qb, int total, float c, bool full,
+                              float* lse, Geom geo, int num_qb, int total, float c, bool full,
                               int variant, hipStream_t s) {
   if (lse) {
-    return full ? launch_fwd<D, CAUSAL, true, true>(q, k, v, o, lse, N, num_qb, total, c, variant, s)
-                : launch_fwd<D, CAUSAL, true, false>(q, k, v, o, lse, N, num_qb, total, c, variant, s);
+    return full ? launch_fwd<D, CAUSAL, true, true>(q, k, v, o, lse, geo, num_qb, total, c, variant, s)
+                : launch_fwd<D, CAUSAL, true, false>(q, k, v, o, lse, geo, num_qb, total, c, variant, s);
   }
-  return full ? launch_fwd<D, CAUSAL, false, true>(q, k, v, o, lse, N, num_qb, total, c, variant, s)
-              : launch_fwd<D, CAUSAL, false, false>(q, k, v, o, lse, N, num_qb, total, c, variant, s);
+  return full ? launch_fwd<D, CAUSAL, false, true>(q, k, v, o, lse, geo, num_qb, total, c, variant, s)
+              : launch_fwd<D, CAUSAL, false, false>(q, k, v, o, lse, geo, num_qb, total, c, variant, s);
 }
 
 // Variant choice (measured on MI355X; see bench.py). The environment
@@ -1093,43 +1143,67 @@ static int choose_variant(int64_t D) {
 }  // namespace fa
 
 namespace fa {
-// The forward with an explicit kernel variant (0: the default choice).
-static int fwd_with_variant(const void* q, const void* k, const void* v, void* o, float* lse,
-                            int64_t B, int64_t H, int64_t N, int64_t D, int causal, int variant,
-                            void* stream) {
-  int st = fa_validate_fwd(q, k, v, o, B, H, N, D);
-  if (st != FA_OK) return st;
-  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
+// The forward over a head geometry with an explicit kernel variant (0: the
+// default choice). Arguments are already validated.
+static int fwd_run(const void* q, const void* k, const void* v, void* o, float* lse,
+                   const Geom& geo, int64_t B, int64_t D, int causal, int variant, void* stream) {
   if (variant == 0) variant = choose_variant(D);
   if (!variant_fits((int)D, variant)) return FA_ERR_HEAD_DIM;
-  const int num_qb = (int)((N + kBR - 1) / kBR);
-  const int total = (int)(B * H * num_qb);
+  const int num_qb = (geo.N + kBR - 1) / kBR;
+  const int total = (int)(B * geo.H * num_qb);
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
-  const bool full = (N % kBR) == 0;
+  const bool full = geo.cu == nullptr && (geo.N % kBR) == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (D == 64) {
-    e = causal ? dispatch_wl<64, true>(q, k, v, o, lse, (int)N, num_qb, total, c, full, variant, s)
-               : dispatch_wl<64, false>(q, k, v, o, lse, (int)N, num_qb, total, c, full, variant, s);
+    e = causal ? dispatch_wl<64, true>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s)
+               : dispatch_wl<64, false>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s);
   } else {
-    e = causal ? dispatch_wl<128, true>(q, k, v, o, lse, (int)N, num_qb, total, c, full, variant, s)
-               : dispatch_wl<128, false>(q, k, v, o, lse, (int)N, num_qb, total, c, full, variant, s);
+    e = causal ? dispatch_wl<128, true>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s)
+               : dispatch_wl<128, false>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s);
   }
   return e == hipSuccess ? FA_OK : -(int)e;
+}
+
+static int fwd_dense(const void* q, const void* k, const void* v, void* o, float* lse,
+                     int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal,
+                     int variant, void* stream) {
+  const int st = fa_validate_fwd_gqa(q, k, v, o, B, H, H_kv, N, D);
+  if (st != FA_OK) return st;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  return fwd_run(q, k, v, o, lse, geo, B, D, causal, variant, stream);
 }
 }  // namespace fa
 
 extern "C" int fa_fwd_f16(const void* q, const void* k, const void* v, void* o,
                           float* lse, int64_t B, int64_t H, int64_t N, int64_t D,
                           int causal, void* stream) {
-  return fa::fwd_with_variant(q, k, v, o, lse, B, H, N, D, causal, 0, stream);
+  return fa::fwd_dense(q, k, v, o, lse, B, H, H, N, D, causal, 0, stream);
+}
+
+extern "C" int fa_fwd_gqa_f16(const void* q, const void* k, const void* v, void* o,
+                              float* lse, int64_t B, int64_t H, int64_t H_kv, int64_t N,
+                              int64_t D, int causal, void* stream) {
+  return fa::fwd_dense(q, k, v, o, lse, B, H, H_kv, N, D, causal, 0, stream);
+}
+
+extern "C" int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, void* o,
+                                 float* lse, const int32_t* cu_seqlens, int64_t B, int64_t H,
+                                 int64_t H_kv, int64_t max_seqlen, int64_t total, int64_t D,
+                                 int causal, void* stream) {
+  const int st = fa_validate_fwd_varlen(q, k, v, o, cu_seqlens, B, H, H_kv, max_seqlen, total, D);
+  if (st != FA_OK) return st;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
+  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total};
+  return fa::fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream);
 }
 
 extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o,
                                     float* lse, int64_t B, int64_t H, int64_t N, int64_t D,
                                     int causal, int variant, void* stream) {
   if (variant <= 0) return FA_ERR_HEAD_DIM;
-  return fa::fwd_with_variant(q, k, v, o, lse, B, H, N, D, causal, variant, stream);
+  return fa::fwd_dense(q, k, v, o, lse, B, H, H, N, D, causal, variant, stream);
 }
 
 extern "C" int fa_probe_default_variant(int64_t D) {

@@ -39,8 +39,12 @@ std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Ten
   const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
   TORCH_CHECK(D == 64 || D == 128, "Head dimension must be 64 or 128");
   TORCH_CHECK(N > 0, "N must be > 0");
-  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes(),
-              "K and V must have the same shape as Q (self-attention only)");
+  TORCH_CHECK(K.dim() == 4 && V.sizes() == K.sizes() && K.size(0) == B && K.size(2) == N &&
+                  K.size(3) == D,
+              "K and V must have the same shape as Q (self-attention only), or [B, H_kv, N, D] "
+              "with H a multiple of H_kv");
+  const int64_t Hkv = K.size(1);
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "H must be a positive multiple of K/V's head count");
   TORCH_CHECK(K.device() == Q.device() && V.device() == Q.device(),
               "Q/K/V must be on the same device");
   TORCH_CHECK(Q.is_floating_point() && K.is_floating_point() && V.is_floating_point(),
@@ -49,8 +53,8 @@ std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Ten
   const c10::DeviceGuard guard(Q.device());
   const int64_t BH = B * H;
   auto Qh = Q.to(torch::kHalf).reshape({BH, N, D}).contiguous();
-  auto Kh = K.to(torch::kHalf).reshape({BH, N, D}).contiguous();
-  auto Vh = V.to(torch::kHalf).reshape({BH, N, D}).contiguous();
+  auto Kh = K.to(torch::kHalf).reshape({B * Hkv, N, D}).contiguous();
+  auto Vh = V.to(torch::kHalf).reshape({B * Hkv, N, D}).contiguous();
   auto O = torch::empty({BH, N, D}, Qh.options());
   torch::Tensor L;
   float* L_ptr = nullptr;
@@ -58,10 +62,11 @@ std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Ten
     L = torch::empty({BH, N}, Qh.options().dtype(torch::kFloat));
     L_ptr = L.data_ptr<float>();
   }
+  TORCH_CHECK(variant == 0 || Hkv == H, "explicit kernel variants take H_kv == H");
   const int st =
       variant == 0
-          ? fa_fwd_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H, N, D,
-                       causal ? 1 : 0, current_stream(Qh))
+          ? fa_fwd_gqa_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H,
+                           Hkv, N, D, causal ? 1 : 0, current_stream(Qh))
           : fa_probe_fwd_variant(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr,
                                  B, H, N, D, causal ? 1 : 0, variant, current_stream(Qh));
   check_status(st, "fa_fwd_f16");
@@ -75,6 +80,40 @@ std::vector<torch::Tensor> forward(torch::Tensor Q, torch::Tensor K, torch::Tens
 
 torch::Tensor forward_only(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bool causal) {
   return forward_impl(Q, K, V, /*want_L=*/false, causal).first;
+}
+
+// forward_varlen(q, k, v, cu_seqlens, max_seqlen, causal=False) -> [O, L]:
+// B packed sequences, head-major: q [H, total, D], k/v [H_kv, total, D],
+// cu_seqlens int32 [B+1]; O [H, total, D] fp16, L [H, total] fp32. Rows of O
+// outside every sequence are left as zeros. No reference counterpart.
+std::vector<torch::Tensor> forward_varlen(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                          torch::Tensor cu_seqlens, int64_t max_seqlen,
+                                          bool causal) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && cu_seqlens.is_cuda(),
+              "q/k/v/cu_seqlens must be CUDA tensors");
+  TORCH_CHECK(q.dim() == 3, "q must be 3D [H, total, D]");
+  const int64_t H = q.size(0), total = q.size(1), D = q.size(2);
+  TORCH_CHECK(k.dim() == 3 && v.sizes() == k.sizes() && k.size(1) == total && k.size(2) == D,
+              "k and v must be [H_kv, total, D] matching q");
+  TORCH_CHECK(cu_seqlens.dim() == 1 && cu_seqlens.scalar_type() == torch::kInt &&
+                  cu_seqlens.size(0) >= 2,
+              "cu_seqlens must be int32 [B + 1]");
+  const auto dev = q.device();
+  TORCH_CHECK(k.device() == dev && v.device() == dev && cu_seqlens.device() == dev,
+              "q/k/v/cu_seqlens must be on the same device");
+  const c10::DeviceGuard guard(dev);
+  const int64_t B = cu_seqlens.size(0) - 1, Hkv = k.size(0);
+  auto qh = q.to(torch::kHalf).contiguous();
+  auto kh = k.to(torch::kHalf).contiguous();
+  auto vh = v.to(torch::kHalf).contiguous();
+  auto cu = cu_seqlens.contiguous();
+  auto O = torch::zeros({H, total, D}, qh.options());
+  auto L = torch::empty({H, total}, qh.options().dtype(torch::kFloat));
+  const int st = fa_fwd_varlen_f16(qh.data_ptr(), kh.data_ptr(), vh.data_ptr(), O.data_ptr(),
+                                   L.data_ptr<float>(), cu.data_ptr<int32_t>(), B, H, Hkv,
+                                   max_seqlen, total, D, causal ? 1 : 0, current_stream(qh));
+  check_status(st, "fa_fwd_varlen_f16");
+  return {O, L};
 }
 
 // backward(Q, K, V, O, dO, L) -> [dQ, dK, dV] float32 [B,H,N,D], the module
@@ -137,7 +176,7 @@ std::vector<int64_t> probe_fwd_variants(int64_t D) {
 }
 
 struct DecodeArgs {
-  int64_t B, H, D, page_size, max_pages, num_pages;
+  int64_t B, H, Hkv, D, page_size, max_pages, num_pages;
 };
 
 DecodeArgs check_decode(const torch::Tensor& q, const torch::Tensor& k_pool,
@@ -164,10 +203,11 @@ DecodeArgs check_decode(const torch::Tensor& q, const torch::Tensor& k_pool,
   a.H = q.size(1);
   a.D = q.size(2);
   a.num_pages = k_pool.size(0);
+  a.Hkv = k_pool.size(1);
   a.page_size = k_pool.size(2);
   a.max_pages = page_table.size(1);
-  TORCH_CHECK(k_pool.size(1) == a.H && k_pool.size(3) == a.D,
-              "k_pool must be [num_pages, H, page_size, D] with q's H and D");
+  TORCH_CHECK(k_pool.size(1) > 0 && a.H % k_pool.size(1) == 0 && k_pool.size(3) == a.D,
+              "k_pool must be [num_pages, H_kv, page_size, D] with q's D and H a multiple of H_kv");
   TORCH_CHECK(page_table.size(0) == a.B && ctx_lens.size(0) == a.B,
               "page_table and ctx_lens must have q's batch size");
   auto dev = q.device();
@@ -181,6 +221,7 @@ std::vector<torch::Tensor> decode_partials(torch::Tensor q, torch::Tensor k_pool
                                            torch::Tensor v_pool, torch::Tensor page_table,
                                            torch::Tensor ctx_lens, int64_t num_splits) {
   const DecodeArgs a = check_decode(q, k_pool, v_pool, page_table, ctx_lens);
+  TORCH_CHECK(a.Hkv == a.H, "decode_partials takes pools with H heads (use decode_paged for GQA)");
   const c10::DeviceGuard guard(q.device());
   auto part_o = torch::empty({a.B, a.H, num_splits, a.D}, q.options().dtype(torch::kFloat));
   auto part_lse = torch::empty({a.B, a.H, num_splits}, q.options().dtype(torch::kFloat));
@@ -223,12 +264,13 @@ std::vector<torch::Tensor> decode_paged(torch::Tensor q, torch::Tensor k_pool, t
   float* part_lse = part_o + a.B * a.H * num_splits * a.D;
   auto o = torch::empty({a.B, a.H, a.D}, q.options());
   auto lse = torch::empty({a.B, a.H}, q.options().dtype(torch::kFloat));
-  const int st = fa_decode_paged_f16(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
-                                     page_table.data_ptr<int32_t>(), ctx_lens.data_ptr<int32_t>(),
-                                     a.B, a.H, a.D, a.page_size, a.max_pages, a.num_pages,
-                                     num_splits, part_o, part_lse, o.data_ptr(),
-                                     lse.data_ptr<float>(), current_stream(q));
-  check_status(st, "fa_decode_paged_f16");
+  const int st = fa_decode_paged_gqa_f16(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                                         page_table.data_ptr<int32_t>(),
+                                         ctx_lens.data_ptr<int32_t>(), a.B, a.H, a.Hkv, a.D,
+                                         a.page_size, a.max_pages, a.num_pages, num_splits, part_o,
+                                         part_lse, o.data_ptr(), lse.data_ptr<float>(),
+                                         current_stream(q));
+  check_status(st, "fa_decode_paged_gqa_f16");
   return {o, lse};
 }
 
@@ -355,6 +397,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
   m.def("forward_only", &forward_only, "FlashAttention forward, O only",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
+  m.def("forward_varlen", &forward_varlen,
+        "packed variable-length forward (head-major): returns [O half, L float]", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("cu_seqlens"), py::arg("max_seqlen"),
+        py::arg("causal") = false);
   m.def("backward", &backward, "FlashAttention backward: returns [dQ, dK, dV] float",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("dO"), py::arg("L"),
         py::arg("causal") = false);

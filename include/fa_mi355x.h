@@ -43,7 +43,8 @@ enum fa_status_code {
   FA_ERR_PAGE_SIZE = 7,      /* page_size is not 16 */
   FA_ERR_NUM_SPLITS = 8,     /* num_splits outside [1, 16] */
   FA_ERR_MAX_PAGES = 9,      /* max_pages <= 0 */
-  FA_ERR_NUM_PAGES = 10      /* num_pages <= 0 */
+  FA_ERR_NUM_PAGES = 10,     /* num_pages <= 0 */
+  FA_ERR_KV_HEADS = 11       /* H_kv <= 0 or H not a multiple of H_kv */
 };
 
 /* Human-readable name of a status code (static storage). */
@@ -73,6 +74,48 @@ int fa_validate_fwd(const void* q, const void* k, const void* v, const void* o,
 int fa_fwd_f16(const void* q, const void* k, const void* v, void* o, float* lse,
                int64_t B, int64_t H, int64_t N, int64_t D, int causal,
                void* stream);
+
+/*
+ * Host-only argument check of fa_fwd_gqa_f16: fa_validate_fwd plus
+ * H_kv > 0 and H % H_kv == 0. No reference counterpart (README.md:326 lists
+ * GQA/MQA as not covered).
+ */
+int fa_validate_fwd_gqa(const void* q, const void* k, const void* v, const void* o,
+                        int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D);
+
+/*
+ * Grouped-query / multi-query forward: q, o fp16 [B, H, N, D]; k, v fp16
+ * [B, H_kv, N, D]; query head h attends with key/value head h / (H / H_kv).
+ * H_kv == H is fa_fwd_f16; H_kv == 1 is MQA. lse, causal and the O-only
+ * contract are those of fa_fwd_f16. No reference counterpart.
+ */
+int fa_fwd_gqa_f16(const void* q, const void* k, const void* v, void* o, float* lse,
+                   int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal,
+                   void* stream);
+
+/*
+ * Host-only argument check of fa_fwd_varlen_f16: pointers (cu_seqlens
+ * 4-byte aligned), D, B/H/H_kv, max_seqlen > 0, total >= 0, index ranges.
+ */
+int fa_validate_fwd_varlen(const void* q, const void* k, const void* v, const void* o,
+                           const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t H_kv,
+                           int64_t max_seqlen, int64_t total, int64_t D);
+
+/*
+ * Variable-length forward over B packed sequences, head-major: q, o fp16
+ * [H, total, D]; k, v fp16 [H_kv, total, D]; lse fp32 [H, total] (or NULL).
+ * Sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1] of every head
+ * (cu_seqlens int32 [B+1], nondecreasing, cu_seqlens[B] <= total) and attends
+ * only within itself (causal: row i of a sequence sees its keys j <= i).
+ * max_seqlen sizes the grid and must be >= every sequence length: rows past
+ * it are not computed. Bounds read from cu_seqlens are clamped into
+ * [0, total], so a malformed table cannot move any access outside the
+ * buffers. No reference counterpart (README.md:326 lists varlen as not
+ * covered).
+ */
+int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, void* o, float* lse,
+                      const int32_t* cu_seqlens, int64_t B, int64_t H, int64_t H_kv,
+                      int64_t max_seqlen, int64_t total, int64_t D, int causal, void* stream);
 
 /*
  * Host-only argument check of fa_bwd_f16. Replaces the checks of the reference
@@ -146,6 +189,18 @@ int fa_decode_paged_f16(const void* q, const void* k_pool, const void* v_pool,
                         int64_t max_pages, int64_t num_pages, int64_t num_splits,
                         float* part_o, float* part_lse, void* o, float* lse,
                         void* stream);
+
+/*
+ * fa_decode_paged_f16 with grouped KV heads: k_pool / v_pool are
+ * [num_pages, H_kv, 16, D] and query head h reads pool head h / (H / H_kv)
+ * (H % H_kv == 0, else FA_ERR_KV_HEADS). part_o / part_lse / o / lse are per
+ * query head, as in fa_decode_paged_f16. No reference counterpart.
+ */
+int fa_decode_paged_gqa_f16(const void* q, const void* k_pool, const void* v_pool,
+                            const int32_t* page_table, const int32_t* ctx_lens, int64_t B,
+                            int64_t H, int64_t H_kv, int64_t D, int64_t page_size,
+                            int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                            float* part_o, float* part_lse, void* o, float* lse, void* stream);
 
 /*
  * Host-only argument check of fa_kv_append_f16. No reference counterpart.

@@ -194,3 +194,44 @@ def test_kv_append_rejects_before_touching_the_device(capi):
     lib = capi.load()
     assert lib.fa_kv_append_f16(*_kv(ps=8), None) == capi.STATUS["FA_ERR_PAGE_SIZE"]
     assert lib.fa_kv_append_f16(*_kv(T=0), None) == capi.STATUS["FA_OK"]   # no launch
+
+
+@pytest.mark.parametrize("args,code", [
+    ((A, A, A, A, 2, 8, 2, 1024, 64), "FA_OK"),
+    ((A, A, A, A, 2, 8, 1, 1024, 128), "FA_OK"),
+    ((A, A, A, A, 2, 8, 3, 1024, 64), "FA_ERR_KV_HEADS"),
+    ((A, A, A, A, 2, 8, 0, 1024, 64), "FA_ERR_KV_HEADS"),
+    ((A, A, A, A, 2, 8, 16, 1024, 64), "FA_ERR_KV_HEADS"),
+    ((A, A, A, A, 2, 8, 2, 1024, 96), "FA_ERR_HEAD_DIM"),
+])
+def test_validate_fwd_gqa(capi, args, code):
+    lib = capi.load()
+    assert lib.fa_validate_fwd_gqa(*args) == capi.STATUS[code]
+
+
+@pytest.mark.parametrize("args,code", [
+    ((A, A, A, A, A, 7, 4, 2, 1024, 1573, 64), "FA_OK"),
+    ((A, A, A, A, A, 7, 4, 2, 1024, 0, 128), "FA_OK"),
+    ((A, A, A, A, 0, 7, 4, 2, 1024, 1573, 64), "FA_ERR_NULL_POINTER"),
+    ((A, A, A, A, A + 2, 7, 4, 2, 1024, 1573, 64), "FA_ERR_ALIGNMENT"),
+    ((A, A, A, A, A, 7, 4, 3, 1024, 1573, 64), "FA_ERR_KV_HEADS"),
+    ((A, A, A, A, A, 7, 4, 2, 0, 1573, 64), "FA_ERR_SEQ_LEN"),
+    ((A, A, A, A, A, 7, 4, 2, 1024, -1, 64), "FA_ERR_SEQ_LEN"),
+    ((A, A, A, A, A, 0, 4, 2, 1024, 1573, 64), "FA_ERR_BATCH_HEADS"),
+    ((A, A, A, A, A, 7, 4, 2, 1 << 24, 1573, 64), "FA_ERR_TOO_LARGE"),
+])
+def test_validate_fwd_varlen(capi, args, code):
+    lib = capi.load()
+    assert lib.fa_validate_fwd_varlen(*args) == capi.STATUS[code]
+
+
+def test_gqa_entry_points_reject_before_touching_the_device(capi):
+    lib = capi.load()
+    assert lib.fa_fwd_gqa_f16(A, A, A, A, None, 1, 8, 3, 64, 64, 0, None) == capi.STATUS["FA_ERR_KV_HEADS"]
+    assert lib.fa_fwd_varlen_f16(A, A, A, A, None, 0, 1, 8, 8, 64, 64, 64, 0, None) == \
+        capi.STATUS["FA_ERR_NULL_POINTER"]
+    args = list(_dec())
+    # (q, k, v, pt, ctx, B, H, D, ps, maxp, np_, S) -> insert H_kv after H
+    gqa = args[:7] + [5] + args[7:] + [A, A, A, None, None]
+    assert lib.fa_decode_paged_gqa_f16(*gqa) == capi.STATUS["FA_ERR_KV_HEADS"]
+    assert lib.fa_status_str(capi.STATUS["FA_ERR_KV_HEADS"]) == b"H must be a positive multiple of H_kv"

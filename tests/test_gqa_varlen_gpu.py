@@ -1,0 +1,142 @@
+"""GPU tier: grouped KV heads (GQA/MQA) and packed variable-length sequences.
+
+Both widen the forward's boundary (README.md:326 lists "varlen, GQA, MQA" as
+not covered by the reference). The expected values come from the pinned
+oracle with no new arithmetic: GQA is naive attention with each KV head
+repeated for its query-head group; varlen is naive attention of each
+sequence on its own. Tolerances are the forward's (tests/test_fwd_gpu.py):
+O max-abs <= 2e-3 plus half an fp16 ulp, L relative <= 1e-4.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode_attention, half_cast, naive_attention
+
+from test_fwd_gpu import _check
+
+pytestmark = pytest.mark.gpu
+
+
+def _randn(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hkv", [1, 2, 8])
+@pytest.mark.parametrize("N,causal", [(128, False), (333, True), (1024, False), (1024, True)])
+def test_gqa_forward(fa, dev, D, Hkv, N, causal):
+    B, H = 2, 8
+    Q = _randn((B, H, N, D), 1)
+    K = _randn((B, Hkv, N, D), 2)
+    V = _randn((B, Hkv, N, D), 3)
+    tq, tk, tv = (torch.from_numpy(x).to(dev) for x in (Q, K, V))
+    O, L = fa.forward(tq, tk, tv, causal=causal)
+    O2 = fa.forward_only(tq, tk, tv, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(O, O2)
+    g = H // Hkv
+    Or, Lr = naive_attention(half_cast(Q), np.repeat(half_cast(K), g, axis=1),
+                             np.repeat(half_cast(V), g, axis=1), causal=causal)
+    _check(O, L, Or, Lr, tag=f"GQA H{H} Hkv{Hkv} N{N} D{D} causal={causal}")
+
+
+def test_gqa_with_all_heads_equals_mha(fa, dev):
+    Q, K, V = (_randn((1, 4, 300, 64), s) for s in (4, 5, 6))
+    tq, tk, tv = (torch.from_numpy(x).to(dev).half() for x in (Q, K, V))
+    O1, L1 = fa.forward(tq, tk, tv)
+    # the same K/V given as a GQA group of 2 that happens to hold equal heads
+    k2 = tk[:, ::2].contiguous()
+    v2 = tv[:, ::2].contiguous()
+    O2, L2 = fa.forward(tq, k2, v2)
+    O3, L3 = fa.forward(tq, k2.repeat_interleave(2, dim=1), v2.repeat_interleave(2, dim=1))
+    assert torch.equal(O2, O3) and torch.equal(L2, L3)
+    assert O1.shape == O2.shape
+
+
+def _cu(lengths):
+    return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Hkv", [4, 2])
+def test_varlen_forward(fa, dev, D, causal, Hkv):
+    H = 4
+    lengths = [1, 100, 0, 257, 1024, 63, 128]
+    cu = _cu(lengths)
+    total = int(cu[-1])
+    q = _randn((H, total, D), 7)
+    k = _randn((Hkv, total, D), 8)
+    v = _randn((Hkv, total, D), 9)
+    tq, tk, tv, tcu = (torch.from_numpy(x).to(dev) for x in (q, k, v, cu))
+    O, L = fa.forward_varlen(tq, tk, tv, tcu, max(lengths), causal=causal)
+    torch.cuda.synchronize()
+    assert O.shape == (H, total, D) and L.shape == (H, total)
+    g = H // Hkv
+    for b, n in enumerate(lengths):
+        if n == 0:
+            continue
+        s0, s1 = cu[b], cu[b + 1]
+        Or, Lr = naive_attention(half_cast(q[None, :, s0:s1]),
+                                 np.repeat(half_cast(k[None, :, s0:s1]), g, axis=1),
+                                 np.repeat(half_cast(v[None, :, s0:s1]), g, axis=1), causal=causal)
+        _check(O[None, :, s0:s1], L[None, :, s0:s1], Or, Lr,
+               tag=f"varlen seq {b} (n={n}) D{D} causal={causal} Hkv{Hkv}")
+
+
+def test_varlen_single_sequence_matches_dense(fa, dev):
+    H, N, D = 2, 512, 64
+    q, k, v = (_randn((H, N, D), s) for s in (10, 11, 12))
+    tq, tk, tv = (torch.from_numpy(x).to(dev).half() for x in (q, k, v))
+    cu = torch.tensor([0, N], dtype=torch.int32, device=dev)
+    Ov, Lv = fa.forward_varlen(tq, tk, tv, cu, N, causal=True)
+    Od, Ld = fa.forward(tq[None], tk[None], tv[None], causal=True)
+    assert (Ov.float() - Od[0].float()).abs().max().item() <= 1e-3
+    assert (Lv - Ld[0]).abs().max().item() <= 1e-4
+
+
+def test_varlen_rows_outside_sequences_and_malformed_bounds(fa, dev):
+    """Trailing rows past cu[B] stay zero; out-of-range bounds are clamped."""
+    H, D = 2, 64
+    total = 300
+    q, k, v = (torch.from_numpy(_randn((H, total, D), s)).to(dev).half() for s in (13, 14, 15))
+    cu = torch.tensor([0, 100, 200], dtype=torch.int32, device=dev)
+    O, L = fa.forward_varlen(q, k, v, cu, 100)
+    assert torch.count_nonzero(O[:, 200:]).item() == 0
+    # decreasing and past-the-end bounds: nothing is read or written outside
+    bad = torch.tensor([0, 250, 100, 10_000], dtype=torch.int32, device=dev)
+    O2, _ = fa.forward_varlen(q, k, v, bad, 256)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O2.float()).all()
+
+
+def test_gqa_decode(fa, dev):
+    B, H, Hkv, D = 4, 8, 2, 128
+    rng = np.random.default_rng(16)
+    ctx = np.array([1, 77, 300, 1000], np.int32)
+    pages = (ctx + 15) // 16
+    table = np.zeros((B, pages.max()), np.int32)
+    perm = rng.permutation(int(pages.sum())).astype(np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    q = rng.standard_normal((B, H, D)).astype(np.float16)
+    kp = rng.standard_normal((int(pages.sum()), Hkv, 16, D)).astype(np.float16)
+    vp = rng.standard_normal((int(pages.sum()), Hkv, 16, D)).astype(np.float16)
+    tq, tkp, tvp, ttab, tctx = (torch.from_numpy(x).to(dev) for x in (q, kp, vp, table, ctx))
+    O, L = fa.decode_paged(tq, tkp, tvp, ttab, tctx, 4)
+    g = H // Hkv
+    Or, Lr = decode_attention(q, np.repeat(kp, g, axis=1), np.repeat(vp, g, axis=1), table, ctx)
+    assert np.abs(O.float().cpu().numpy() - Or).max() <= 2e-3
+    assert (np.abs(L.cpu().numpy() - Lr) / np.maximum(np.abs(Lr), 1)).max() <= 1e-4
+    with pytest.raises(RuntimeError, match="decode_partials takes pools with H heads"):
+        fa.decode_partials(tq, tkp, tvp, ttab, tctx, 4)
+
+
+def test_gqa_rejects_bad_head_counts(fa, dev):
+    q = torch.zeros(1, 6, 64, 64, device=dev)
+    kv = torch.zeros(1, 4, 64, 64, device=dev)
+    with pytest.raises(RuntimeError, match="multiple"):
+        fa.forward(q, kv, kv)
