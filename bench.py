@@ -1,7 +1,7 @@
 """Benchmark: FlashAttention forward TFLOP/s (and % of dense FP16 MFMA peak) at
 B=1 H=8 N=4096 D=64 on one MI355X, plus the split-KV paged decode in GB/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|widen|copy]
 
 A step is one ``forward(Q, K, V)`` call (O fp16 + L fp32) of the headline
 configuration (N=4096) on inputs resident in HBM.
@@ -251,6 +251,33 @@ def bench_sdpa(fa, torch, dev, reps=10):
     return res
 
 
+def bench_widen(fa, torch, dev, reps=5, iters=50):
+    """The generality row: bf16 and GQA forward at the headline shape, and a
+    packed varlen batch with the headline's total work."""
+    res = {}
+    B, H, N, D = 1, 8, 4096, 64
+    g = torch.Generator(device=dev).manual_seed(21)
+    q, k, v = (torch.randn(B, H, N, D, device=dev, generator=g).bfloat16() for _ in range(3))
+    ms = median_of(lambda: fa.forward_bf16(q, k, v), reps, 10, iters, torch)
+    f = fwd_flops(B, H, N, D)
+    res["bf16_B1H8N4096D64"] = {"ms": round(ms, 5), "TFLOPs": round(f / ms / 1e9, 1),
+                                "pct_peak": round(100 * f / ms / 1e9 / PEAK_FP16_TFLOPS, 2)}
+    qh = q.half()
+    kh, vh = k[:, :2].half().contiguous(), v[:, :2].half().contiguous()
+    ms = median_of(lambda: fa.forward(qh, kh, vh), reps, 10, iters, torch)
+    res["gqa_H8_Hkv2_N4096D64"] = {"ms": round(ms, 5), "TFLOPs": round(f / ms / 1e9, 1)}
+    # 8 sequences of 512 .. 7680 rows (4096 on average), H8 D64, head-major packed
+    lens = [512, 7680, 1024, 7168, 2048, 6144, 3072, 5120]
+    cu = torch.tensor([0] + list(__import__("itertools").accumulate(lens)), dtype=torch.int32,
+                      device=dev)
+    total = sum(lens)
+    qv, kv_, vv = (torch.randn(H, total, D, device=dev, generator=g).half() for _ in range(3))
+    ms = median_of(lambda: fa.forward_varlen(qv, kv_, vv, cu, max(lens)), reps, 5, 20, torch)
+    fv = sum(4.0 * H * n * n * D for n in lens)
+    res["varlen_H8D64_8seqs_total32768"] = {"ms": round(ms, 5), "TFLOPs": round(fv / ms / 1e9, 1)}
+    return res
+
+
 def cpu_baseline(budget_s=20.0):
     """Numpy oracle on the headline workload, bounded: whole heads until ~budget_s."""
     import numpy as np
@@ -314,7 +341,8 @@ def main():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "pages", "sdpa", "copy"],
+    ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "pages", "sdpa", "widen",
+                                       "copy"],
                     default="all")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
@@ -342,6 +370,9 @@ def main():
         return
     if args.only == "pages":
         print(json.dumps({"kv_append": bench_pages(fa, torch, dev)}))
+        return
+    if args.only == "widen":
+        print(json.dumps({"widen": bench_widen(fa, torch, dev)}))
         return
     if args.only == "sdpa":
         print(json.dumps({"sdpa_comparator": bench_sdpa(fa, torch, dev)}))
@@ -419,6 +450,7 @@ def main():
         out["backward"] = bench_backward(fa, torch, dev)
         out["kv_append"] = bench_pages(fa, torch, dev)
         out["sdpa_comparator"] = bench_sdpa(fa, torch, dev)
+        out["widen"] = bench_widen(fa, torch, dev)
         out["copy_calibration"] = copy_calibration(torch, dev)
     if not args.no_cpu and args.only == "all":
         out["cpu_baseline"] = cpu_baseline(args.cpu_budget)

@@ -59,6 +59,11 @@ def forward(Q, K, V, causal: bool = False):
     return _C.forward(Q, K, V, causal)
 
 
+def forward_bf16(Q, K, V, causal: bool = False, want_L: bool = True):
+    """bfloat16 forward: [O bf16 [B,H,N,D], L fp32 [B,H,N]] ([O] if not want_L)."""
+    return _C.forward_bf16(Q, K, V, causal, want_L)
+
+
 def forward_varlen(q, k, v, cu_seqlens, max_seqlen: int, causal: bool = False):
     """[O, L] of B packed sequences, head-major: q [H, total, D], k/v [H_kv, total, D].
 

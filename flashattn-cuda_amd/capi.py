@@ -40,6 +40,7 @@ SIGNATURES = {
     "fa_bwd_f16": (C.c_int, [_vp] * 10 + [_i64] * 4 + [C.c_int, _vp]),
     "fa_validate_fwd_gqa": (C.c_int, [_vp] * 4 + [_i64] * 5),
     "fa_fwd_gqa_f16": (C.c_int, [_vp] * 5 + [_i64] * 5 + [C.c_int, _vp]),
+    "fa_fwd_bf16": (C.c_int, [_vp] * 5 + [_i64] * 5 + [C.c_int, _vp]),
     "fa_validate_fwd_varlen": (C.c_int, [_vp] * 5 + [_i64] * 6),
     "fa_fwd_varlen_f16": (C.c_int, [_vp] * 6 + [_i64] * 6 + [C.c_int, _vp]),
     "fa_decode_paged_gqa_f16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 5),

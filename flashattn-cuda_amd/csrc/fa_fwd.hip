@@ -102,7 +102,7 @@ __device__ __forceinline__ HeadView head_view(const Geom& g, int bh) {
 
 // State and tile operations of one wave: 32 query rows, one lane pair per row
 // (lanes l and l^32 hold the two halves of every 32-key block).
-template <int D, bool CAUSAL, bool FULL>
+template <int D, bool CAUSAL, bool FULL, bool BF16 = false>
 struct RowBlock {
   static constexpr int KSTEPS = D / 16;   // QK k-steps
   static constexpr int DB = D / 32;       // O^T d-blocks
@@ -152,7 +152,7 @@ struct RowBlock {
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) s[b] = mfma32(load_k_frag<D>(ks, kb0 + b, kk, lane), qf[kk], s[b]);
+      for (int b = 0; b < NB; ++b) s[b] = mma32<BF16>(load_k_frag<D>(ks, kb0 + b, kk, lane), qf[kk], s[b]);
     }
   }
 
@@ -202,7 +202,7 @@ struct RowBlock {
           const float e0 = exp2_hw(fmaf(s[b][r], c, -m));
           const float e1 = exp2_hw(fmaf(s[b][r + 1], c, -m));
           acc[q] += e0 + e1;
-          x[q] = cvt2(e0, e1);
+          x[q] = cvt2x<BF16>(e0, e1);
         }
         pf[2 * b + h] = f16x8{x[0][0], x[0][1], x[1][0], x[1][1], x[2][0], x[2][1], x[3][0], x[3][1]};
       }
@@ -257,7 +257,7 @@ struct RowBlock {
     for (int j = 0; j < 2 * NB; ++j) {
 #pragma unroll
       for (int db = 0; db < DB; ++db)
-        o[db] = mfma32(load_v_frag<D>(vs, 2 * kb0 + j, db, lane), pf[j], o[db]);
+        o[db] = mma32<BF16>(load_v_frag<D>(vs, 2 * kb0 + j, db, lane), pf[j], o[db]);
     }
   }
 
@@ -298,8 +298,8 @@ struct RowBlock {
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          f16x2 a = cvt2(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv);
-          f16x2 b = cvt2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+          f16x2 a = cvt2x<BF16>(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv);
+          f16x2 b = cvt2x<BF16>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
           f16x4 v4 = f16x4{a[0], a[1], b[0], b[1]};
           *reinterpret_cast<f16x4*>(orow + 32 * db + 8 * g + 4 * hi) = v4;
         }
@@ -360,7 +360,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the copies hide (all workgroups of a head request the same tile at about
 // the same time, so a tile's first fetch is a miss for all of them).
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES, bool BF16 = false>
 __global__ void __launch_bounds__(256 * KSPLIT)
 fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                     const f16* __restrict__ V, f16* __restrict__ O,
@@ -373,7 +373,7 @@ fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int PER_GROUP = 2 * LOADS;                    // copies per wave per group
   static_assert(STAGES >= 2 && STAGES <= 4, "two to four stages");
   static_assert(2 * STAGES * GROUP <= 160 * 1024, "stages exceed the 160 KiB LDS");
-  using RB = RowBlock<D, CAUSAL, FULL>;
+  using RB = RowBlock<D, CAUSAL, FULL, BF16>;
   static_assert((KSPLIT - 1) * (2 + 16 * RB::DB) * 64 * 4 <= GROUP, "merge area too small");
   // Stage s: K part at 2*s*GROUP, V part at (2*s+1)*GROUP; each KSPLIT tiles.
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGES * GROUP];
@@ -1040,10 +1040,10 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 constexpr int kPingPong = 204;
 constexpr int pipe_code(int ksplit, int ring) { return 100 + 10 * ring + ksplit; }
 
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES, bool BF16 = false>
 static void launch_split(const f16* Q, const f16* K, const f16* V, f16* O, float* L, Geom geo,
                          int num_qb, int total, float c, hipStream_t stream) {
-  hipLaunchKernelGGL((fa_fwd_split_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, STAGES>), dim3(total),
+  hipLaunchKernelGGL((fa_fwd_split_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, STAGES, BF16>), dim3(total),
                      dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, geo, num_qb, total, c);
 }
 
@@ -1197,6 +1197,61 @@ extern "C" int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, vo
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
   const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total};
   return fa::fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream);
+}
+
+namespace fa {
+// bfloat16 forward: the default split variant of each D with bf16 operands
+// (v_mfma_f32_32x32x16_bf16, P packed with v_cvt_pk_bf16_f32).
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL>
+static void launch_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                        const Geom& geo, int num_qb, int total, float c, hipStream_t s) {
+  const f16* Q = (const f16*)q;
+  const f16* K = (const f16*)k;
+  const f16* V = (const f16*)v;
+  f16* O = (f16*)o;
+  if constexpr (D == 64) {
+    launch_split<D, CAUSAL, WRITE_L, FULL, 4, 2, true>(Q, K, V, O, lse, geo, num_qb, total, c, s);
+  } else {
+    launch_split<D, CAUSAL, WRITE_L, FULL, 1, 2, true>(Q, K, V, O, lse, geo, num_qb, total, c, s);
+  }
+}
+
+template <int D, bool CAUSAL>
+static void dispatch_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                          const Geom& geo, int num_qb, int total, float c, bool full,
+                          hipStream_t s) {
+  if (lse) {
+    if (full) launch_bf16<D, CAUSAL, true, true>(q, k, v, o, lse, geo, num_qb, total, c, s);
+    else launch_bf16<D, CAUSAL, true, false>(q, k, v, o, lse, geo, num_qb, total, c, s);
+  } else {
+    if (full) launch_bf16<D, CAUSAL, false, true>(q, k, v, o, lse, geo, num_qb, total, c, s);
+    else launch_bf16<D, CAUSAL, false, false>(q, k, v, o, lse, geo, num_qb, total, c, s);
+  }
+}
+}  // namespace fa
+
+extern "C" int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                           int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal,
+                           void* stream) {
+  using namespace fa;
+  const int st = fa_validate_fwd_gqa(q, k, v, o, B, H, H_kv, N, D);
+  if (st != FA_OK) return st;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  const int num_qb = (int)((N + kBR - 1) / kBR);
+  const int total = (int)(B * H * num_qb);
+  const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  const bool full = (N % kBR) == 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (D == 64) {
+    if (causal) dispatch_bf16<64, true>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
+    else dispatch_bf16<64, false>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
+  } else {
+    if (causal) dispatch_bf16<128, true>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
+    else dispatch_bf16<128, false>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FA_OK : -(int)e;
 }
 
 extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o,

@@ -41,6 +41,20 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Operand registers hold raw 16-bit values; BF16 selects how they are read.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <bool BF16>
+__device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return mfma32(a, b, c);
+  }
+}
+
 // 2^x on the hardware transcendental unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 // log2(x) on v_log_f32.
@@ -227,6 +241,17 @@ __device__ __forceinline__ int st_key(int kb, int r, int lane) {
 // fp32 -> fp16 round-to-nearest-even, two at a time (v_cvt_pk_f16_f32).
 __device__ __forceinline__ f16x2 cvt2(float a, float b) {
   return f16x2{(f16)a, (f16)b};
+}
+
+// fp32 -> 16-bit operand pair: fp16 (v_cvt_pk_f16_f32) or, with BF16,
+// bfloat16 round-to-nearest-even (v_cvt_pk_bf16_f32), as raw bits.
+template <bool BF16>
+__device__ __forceinline__ f16x2 cvt2x(float a, float b) {
+  if constexpr (BF16) {
+    return __builtin_bit_cast(f16x2, bf16x2{(__bf16)a, (__bf16)b});
+  } else {
+    return cvt2(a, b);
+  }
 }
 
 // B operand (P^T) of PV k-step j from the S^T accumulators p[2] of a tile.

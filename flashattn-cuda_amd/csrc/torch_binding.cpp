@@ -82,6 +82,41 @@ torch::Tensor forward_only(torch::Tensor Q, torch::Tensor K, torch::Tensor V, bo
   return forward_impl(Q, K, V, /*want_L=*/false, causal).first;
 }
 
+// forward_bf16(Q, K, V, causal=False) -> [O bf16, L float]: the bfloat16
+// forward (K/V may have fewer heads, GQA). Inputs are cast to bf16. No
+// reference counterpart (the reference module is fp16-only).
+std::vector<torch::Tensor> forward_bf16(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                        bool causal, bool want_L) {
+  TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Q/K/V must be CUDA tensors");
+  TORCH_CHECK(Q.dim() == 4, "Q must be 4D [B, H, N, D]");
+  const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
+  TORCH_CHECK(D == 64 || D == 128, "Head dimension must be 64 or 128");
+  TORCH_CHECK(N > 0, "N must be > 0");
+  TORCH_CHECK(K.dim() == 4 && V.sizes() == K.sizes() && K.size(0) == B && K.size(2) == N &&
+                  K.size(3) == D,
+              "K and V must be [B, H_kv, N, D] with H a multiple of H_kv");
+  const int64_t Hkv = K.size(1);
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "H must be a positive multiple of K/V's head count");
+  TORCH_CHECK(K.device() == Q.device() && V.device() == Q.device(),
+              "Q/K/V must be on the same device");
+  const c10::DeviceGuard guard(Q.device());
+  auto q = Q.to(torch::kBFloat16).contiguous();
+  auto k = K.to(torch::kBFloat16).contiguous();
+  auto v = V.to(torch::kBFloat16).contiguous();
+  auto O = torch::empty({B, H, N, D}, q.options());
+  torch::Tensor L;
+  float* L_ptr = nullptr;
+  if (want_L) {
+    L = torch::empty({B, H, N}, q.options().dtype(torch::kFloat));
+    L_ptr = L.data_ptr<float>();
+  }
+  const int st = fa_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), L_ptr, B, H,
+                             Hkv, N, D, causal ? 1 : 0, current_stream(q));
+  check_status(st, "fa_fwd_bf16");
+  if (want_L) return {O, L};
+  return {O};
+}
+
 // forward_varlen(q, k, v, cu_seqlens, max_seqlen, causal=False) -> [O, L]:
 // B packed sequences, head-major: q [H, total, D], k/v [H_kv, total, D],
 // cu_seqlens int32 [B+1]; O [H, total, D] fp16, L [H, total] fp32. Rows of O
@@ -397,6 +432,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
   m.def("forward_only", &forward_only, "FlashAttention forward, O only",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false);
+  m.def("forward_bf16", &forward_bf16, "bfloat16 forward: returns [O bf16, L float] ([O] if not want_L)",
+        py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("causal") = false,
+        py::arg("want_L") = true);
   m.def("forward_varlen", &forward_varlen,
         "packed variable-length forward (head-major): returns [O half, L float]", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("cu_seqlens"), py::arg("max_seqlen"),

@@ -94,6 +94,16 @@ int fa_fwd_gqa_f16(const void* q, const void* k, const void* v, void* o, float* 
                    void* stream);
 
 /*
+ * bfloat16 forward: q, o bf16 [B, H, N, D]; k, v bf16 [B, H_kv, N, D]
+ * (H_kv == H for plain multi-head); fp32 accumulation and softmax, P rounded
+ * to bf16 for the PV product; lse fp32 [B, H, N] or NULL (O-only, bitwise the
+ * same o). Same argument checks as fa_fwd_gqa_f16. No reference counterpart
+ * (the reference is fp16-only).
+ */
+int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal, void* stream);
+
+/*
  * Host-only argument check of fa_fwd_varlen_f16: pointers (cu_seqlens
  * 4-byte aligned), D, B/H/H_kv, max_seqlen > 0, total >= 0, index ranges.
  */

@@ -33,6 +33,8 @@ Pinning status (each function is checked in tests/test_oracle.py):
   over the contiguous keys; gather equals a direct index walk.
 * split_partials + lse_combine: combine of any split count equals the
   unsplit result; one split is the identity; empty splits carry weight 0.
+* bf16_cast: against torch's CPU bfloat16 conversion on random, tie and
+  boundary values.
 * append_pages: appending a prefill into an empty pool and reading it back
   with gather_pages returns the rows (gather_pages is itself pinned by an
   explicit index walk); appending in two steps equals one step; invalid page
@@ -53,6 +55,16 @@ LN2 = math.log(2.0)
 def half_cast(x: np.ndarray) -> np.ndarray:
     """fp16 round-trip then float32, the cast of tests/test_fa3_db_full.py:34."""
     return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def bf16_cast(x: np.ndarray) -> np.ndarray:
+    """bfloat16 round trip (round to nearest, ties to even) then float32.
+
+    The input rounding of the bf16 forward; finite inputs only.
+    """
+    a = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (a + 0x7FFF + ((a >> 16) & 1)) >> 16 << 16
+    return r.astype(np.uint32).view(np.float32).reshape(np.shape(x))
 
 
 def _softmax_lse(S: np.ndarray):

@@ -472,3 +472,24 @@ def test_planted_append_mistakes_are_caught(mistake):
     ok = all(np.array_equal(orc.gather_pages(bad_kp, table, T, b, h), kn[b, h])
              for b in range(B) for h in range(H))
     assert not ok
+
+
+# ---------------------------------------------------------------- bf16 rounding
+def test_bf16_cast_matches_torch_and_ties_to_even():
+    import torch
+    rng = np.random.default_rng(12)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 10.0 ** rng.integers(-6, 6, 10000),
+                        np.array([0.0, -0.0, 1.0, 65504.0, 3.0e38, 1e-40], np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(orc.bf16_cast(x), ref)
+    # exact ties: 1 + 2^-8 lies halfway between 1 and 1 + 2^-7 -> even (1.0);
+    # 1 + 3 * 2^-8 lies halfway between 1 + 2^-7 and 1 + 2^-6 -> even (1 + 2^-6)
+    ties = np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8], np.float32)
+    np.testing.assert_array_equal(orc.bf16_cast(ties), np.array([1.0, 1 + 2.0 ** -6], np.float32))
+
+
+def test_planted_bf16_truncation_is_caught():
+    import torch
+    x = np.random.default_rng(13).standard_normal(1000).astype(np.float32)
+    trunc = (x.view(np.uint32) >> 16 << 16).view(np.float32)   # round toward zero
+    assert not np.array_equal(trunc, torch.from_numpy(x).to(torch.bfloat16).float().numpy())
