@@ -19,14 +19,20 @@
 //     running max m; the lane's tile sum bounds every P it holds, and only when
 //     it exceeds 2^15 (first tile, or a much larger new maximum) is m raised
 //     and O rescaled. P <= 2^15 stays inside fp16 and the fp32 accumulators.
-// Two kernels share that per-wave core (RowBlock):
+// Three kernels share that per-wave core (RowBlock):
+//   * fa_fwd_pp_kernel (the default): two wave groups own the even and odd
+//     key tiles of the same rows and alternate, barrier by barrier, between a
+//     matrix phase and a softmax phase, so each SIMD runs one wave's MFMAs
+//     while the other wave's VALU work issues;
 //   * fa_fwd_split_kernel<.., KSPLIT>: 4*KSPLIT waves; the KSPLIT waves of a
 //     row group take every KSPLIT-th tile and merge their (m, l, O) through LDS
-//     at the end. More waves per SIMD is what lets MFMA and VALU work of
-//     different waves overlap (a single wave issues VALU work several times
-//     slower than four waves sharing a SIMD);
+//     at the end (also the bf16 path);
 //   * fa_fwd_pipe_kernel: one wave per row group, software-pipelined (QK of
 //     tile t+1 issued alongside the softmax of tile t).
+// A single wave issues VALU work about half as fast as two or more waves
+// sharing a SIMD (measured: fp32 fma 2.8 ns vs 1.3-1.5 ns per instruction,
+// v_exp_f32 6.7 ns vs 4.0-4.6 ns), which is what all three designs work
+// around.
 // Template flags: D in {64,128}, CAUSAL, WRITE_L (O-only when false), FULL
 // (N % 128 == 0: no bounds predicates).
 #include <hip/hip_runtime.h>
@@ -824,6 +830,7 @@ __global__ void __launch_bounds__(512)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
                  float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
+  constexpr int TPS = 2;                       // tiles per step (one per group)
   static_assert(RING == 4 || RING == 6, "an even ring of four or six tiles");
   constexpr int TILE = kBC * D * 2;
   constexpr int BLOCKS = TILE / 1024;          // 1 KiB blocks per tile
@@ -833,7 +840,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int DB = RB::DB;
   constexpr int KSTEPS = D / 16;
   constexpr int NMM = D / 8;                   // MFMAs of one QK (= of one PV)
-  constexpr int PF = 4;                        // operand prefetch distance, in MFMAs
+  constexpr int PF = D == 64 ? 8 : 4;          // operand prefetch distance, in MFMAs
   constexpr int REC = (2 + 16 * DB) * 64;      // floats per wave record of the merge
   static_assert(kRowGroups * REC * 4 <= 2 * RING * TILE, "merge area too small");
   // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
@@ -844,6 +851,8 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: SGPR
   const int rg = wave & (kRowGroups - 1);
   const int grp = wave >> 2;
+  // Tile of group g in step j.
+  auto tile_of = [&](int g, int j) { return TPS * j + g; };
 
   const int logical = xcd_remap(blockIdx.x, total);
   const int bh = logical / num_qb;
@@ -864,7 +873,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 
   const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
   const int n_tiles = (kv_end + kBC - 1) / kBC;
-  const int n_steps = (n_tiles + 1) / 2;       // tiles per group
+  const int n_steps = (n_tiles + TPS - 1) / TPS;   // tiles per group
 
   const uint32_t lds0 = lds_addr(smem);
   // This wave's share of a tile copy in its M phase: blocks rg*LOADS .. +LOADS.
@@ -992,33 +1001,51 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     rb.l_run += rs;
     // This wave's copies of its M phase RING/2 - 1 phases of its own back;
     // those of the later M phases stay in flight.
-    wait_vmcnt<(RING / 2 - 2) * 2 * LOADS>();
+    wait_vmcnt<(RING / TPS - 2) * 2 * LOADS>();
   };
 
+  // A phase's register-only work must stay between its barriers: the compiler
+  // may otherwise move a softmax across the barrier into the other group's
+  // matrix phase. The empty volatile asm ties the scores to a point after the
+  // barrier and P to a point before the next one.
+  auto pin_s = [&] { asm volatile("" : "+v"(s[0]), "+v"(s[1])); };
+  auto pin_p = [&] { asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3])); };
+  // M phase copies: K and V of the tiles RING - TPS after the ones it reads.
+  auto mstep = [&](auto with_pv, int tq, int tv) {
+    mphase(with_pv, tq, tv, tq + RING - TPS, tv + RING - TPS);
+  };
   if (grp == 0) {
-    rb.template qk<2>(smem, 0, s);   // tile 0 (slot 0)
-    __syncthreads();                 // slot 0 is refilled in phase 1
+    rb.template qk<2>(smem + (tile_of(0, 0) % RING) * TILE, 0, s);
+    __syncthreads();                 // its slot is refilled in phase 1
     for (int j = 0; j < n_steps; ++j) {
-      sphase(2 * j);
+      pin_s();
+      sphase(tile_of(0, j));
+      pin_p();
       __syncthreads();
-      mphase(BT{}, 2 * j + 2, 2 * j, 2 * j + RING, 2 * j + RING - 2);
+      mstep(BT{}, tile_of(0, j + 1), tile_of(0, j));
       __syncthreads();
     }
     __syncthreads();   // group 1's last PV
   } else {
     __syncthreads();
-    for (int j = 0; j < n_steps; ++j) {
-      if (j == 0) {
-        mphase(BF{}, 1, 0, RING - 1, RING - 3);
-      } else {
-        mphase(BT{}, 2 * j + 1, 2 * j - 1, 2 * j + RING - 1, 2 * j + RING - 3);
-      }
+    // Step 0 (no PV yet) is peeled: with both M-phase forms in one loop body
+    // the compiler moved the accumulators between them on every step.
+    mstep(BF{}, tile_of(1, 0), tile_of(1, -1));
+    __syncthreads();
+    pin_s();
+    sphase(tile_of(1, 0));
+    pin_p();
+    __syncthreads();
+    for (int j = 1; j < n_steps; ++j) {
+      mstep(BT{}, tile_of(1, j), tile_of(1, j - 1));
       __syncthreads();
-      sphase(2 * j + 1);
+      pin_s();
+      sphase(tile_of(1, j));
+      pin_p();
       __syncthreads();
     }
     // Phase 2n: the last PV.
-    rb.template pv<2>(smem + (RING + (2 * n_steps - 1) % RING) * TILE, 0, p);
+    rb.template pv<2>(smem + (RING + tile_of(1, n_steps - 1) % RING) * TILE, 0, p);
     __syncthreads();
   }
   wait_vmem();   // copies of the last M phases
@@ -1134,10 +1161,10 @@ static int choose_variant(int64_t D) {
     return -1;
   }();
   if (forced >= 0 && variant_fits((int)D, forced)) return forced;
-  // D = 64: four key slices per query block (16 waves per workgroup) keep
-  // every SIMD busy even when B*H*N/128 is about one workgroup per CU.
-  // D = 128: one slice, double-buffered; the larger tiles already fill it.
-  return D == 64 ? 42 : 12;
+  // The ping-pong kernel (ring of 4 tiles) is fastest at every measured
+  // shape, D = 64 and 128, causal or not: one wave of each SIMD runs its
+  // matrix phase while the other runs its softmax.
+  return kPingPong;
 }
 
 }  // namespace fa
