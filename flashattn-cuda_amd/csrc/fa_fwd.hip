@@ -26,7 +26,7 @@
 //     while the other wave's VALU work issues;
 //   * fa_fwd_split_kernel<.., KSPLIT>: 4*KSPLIT waves; the KSPLIT waves of a
 //     row group take every KSPLIT-th tile and merge their (m, l, O) through LDS
-//     at the end (also the bf16 path);
+//     at the end;
 //   * fa_fwd_pipe_kernel: one wave per row group, software-pipelined (QK of
 //     tile t+1 issued alongside the softmax of tile t).
 // A single wave issues VALU work about half as fast as two or more waves
@@ -366,7 +366,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the copies hide (all workgroups of a head request the same tile at about
 // the same time, so a tile's first fetch is a miss for all of them).
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES, bool BF16 = false>
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
 __global__ void __launch_bounds__(256 * KSPLIT)
 fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                     const f16* __restrict__ V, f16* __restrict__ O,
@@ -379,7 +379,7 @@ fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int PER_GROUP = 2 * LOADS;                    // copies per wave per group
   static_assert(STAGES >= 2 && STAGES <= 4, "two to four stages");
   static_assert(2 * STAGES * GROUP <= 160 * 1024, "stages exceed the 160 KiB LDS");
-  using RB = RowBlock<D, CAUSAL, FULL, BF16>;
+  using RB = RowBlock<D, CAUSAL, FULL>;
   static_assert((KSPLIT - 1) * (2 + 16 * RB::DB) * 64 * 4 <= GROUP, "merge area too small");
   // Stage s: K part at 2*s*GROUP, V part at (2*s+1)*GROUP; each KSPLIT tiles.
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGES * GROUP];
@@ -825,7 +825,7 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // RING/2 - 1 steps to land. Tiles past the end are copied with an empty
 // buffer range (zeros).
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING>
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false>
 __global__ void __launch_bounds__(512)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
@@ -836,7 +836,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int BLOCKS = TILE / 1024;          // 1 KiB blocks per tile
   constexpr int LOADS = BLOCKS / 4;            // blocks per M-phase wave per tile
   static_assert(2 * RING * TILE <= 160 * 1024, "slots exceed the 160 KiB LDS");
-  using RB = RowBlock<D, CAUSAL, FULL>;
+  using RB = RowBlock<D, CAUSAL, FULL, BF16>;
   constexpr int DB = RB::DB;
   constexpr int KSTEPS = D / 16;
   constexpr int NMM = D / 8;                   // MFMAs of one QK (= of one PV)
@@ -956,9 +956,9 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       if constexpr (m + PF < NM) op[m + PF] = fetch(m + PF);
       constexpr int i = PV ? m >> 1 : m;
       if constexpr (PV && (m & 1) == 0) {
-        rb.o[i % DB] = mfma32(op[m], p[i / DB], rb.o[i % DB]);
+        rb.o[i % DB] = mma32<BF16>(op[m], p[i / DB], rb.o[i % DB]);
       } else {
-        s[i % 2] = mfma32(op[m], rb.qf[i / 2], s[i % 2]);
+        s[i % 2] = mma32<BF16>(op[m], rb.qf[i / 2], s[i % 2]);
       }
       // Copy c of this phase after MFMA (c + 1) * NM / (NC + 1).
       static_for<0, NC>([&](auto ci) {
@@ -985,7 +985,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       }
       if constexpr (u >= 2) {
         constexpr int q2 = u - 2, b = q2 / 8, h = (q2 % 8) / 4, q = q2 % 4;
-        const f16x2 x = cvt2(ex[q2][0], ex[q2][1]);
+        const f16x2 x = cvt2x<BF16>(ex[q2][0], ex[q2][1]);
         if constexpr (q2 < 2) {
           acc[q2] = ex[q2][0] + ex[q2][1];
         } else {
@@ -1067,10 +1067,10 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 constexpr int kPingPong = 204;
 constexpr int pipe_code(int ksplit, int ring) { return 100 + 10 * ring + ksplit; }
 
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES, bool BF16 = false>
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
 static void launch_split(const f16* Q, const f16* K, const f16* V, f16* O, float* L, Geom geo,
                          int num_qb, int total, float c, hipStream_t stream) {
-  hipLaunchKernelGGL((fa_fwd_split_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, STAGES, BF16>), dim3(total),
+  hipLaunchKernelGGL((fa_fwd_split_kernel<D, CAUSAL, WRITE_L, FULL, KSPLIT, STAGES>), dim3(total),
                      dim3(256 * KSPLIT), 0, stream, Q, K, V, O, L, geo, num_qb, total, c);
 }
 
@@ -1227,7 +1227,7 @@ extern "C" int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, vo
 }
 
 namespace fa {
-// bfloat16 forward: the default split variant of each D with bf16 operands
+// bfloat16 forward: the default (ping-pong) kernel with bf16 operands
 // (v_mfma_f32_32x32x16_bf16, P packed with v_cvt_pk_bf16_f32).
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL>
 static void launch_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -1236,11 +1236,8 @@ static void launch_bf16(const void* q, const void* k, const void* v, void* o, fl
   const f16* K = (const f16*)k;
   const f16* V = (const f16*)v;
   f16* O = (f16*)o;
-  if constexpr (D == 64) {
-    launch_split<D, CAUSAL, WRITE_L, FULL, 4, 2, true>(Q, K, V, O, lse, geo, num_qb, total, c, s);
-  } else {
-    launch_split<D, CAUSAL, WRITE_L, FULL, 1, 2, true>(Q, K, V, O, lse, geo, num_qb, total, c, s);
-  }
+  hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4, true>), dim3(total), dim3(512), 0,
+                     s, Q, K, V, O, lse, geo, num_qb, total, c);
 }
 
 template <int D, bool CAUSAL>
