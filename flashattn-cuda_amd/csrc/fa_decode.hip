@@ -151,6 +151,153 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
   }
 }
 
+// Grouped-KV split pass: one workgroup per (split, G query heads that share
+// one KV head, sequence). Each K/V page is loaded once into registers and
+// used for all G heads (a lane's dot products, softmax state and output
+// slice are kept per head), so a page is read once per KV head instead of
+// once per query head. Waves split the pages as above and merge per head.
+template <int D, int G>
+__global__ void __launch_bounds__(kDecThreads)
+fa_decode_split_group_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
+                             const f16* __restrict__ vpool, const int32_t* __restrict__ page_table,
+                             const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
+                             float* __restrict__ part_lse, int H, int Hkv, int max_pages,
+                             int num_pages, int S, float c) {
+  constexpr int DPL = D / 4;   // d per lane
+  constexpr int NV = DPL / 8;  // 16-byte vectors per lane per row
+  __shared__ float sh_o[kDecWaves][G][D];
+  __shared__ float sh_m[kDecWaves][G];
+  __shared__ float sh_l[kDecWaves][G];
+  __shared__ int sh_bad;
+
+  const int s = blockIdx.x, hg = blockIdx.y, b = blockIdx.z;
+  const int h0 = hg * G;                  // first query head of this workgroup
+  const int hk = h0 / (H / Hkv);          // their KV head (G divides H / Hkv)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tok = lane >> 2;
+  const int dq = lane & 3;
+
+  if (tid == 0) sh_bad = 0;
+  __syncthreads();
+
+  int ctx = ctx_lens[b];
+  bool bad = false;
+  if (ctx < 0) { bad = true; ctx = 0; }
+  int pages = (ctx + kPage - 1) / kPage;
+  if (pages > max_pages) { bad = true; pages = max_pages; ctx = max_pages * kPage; }
+  const int chunk = (pages + S - 1) / S;
+  const int p0 = min(s * chunk, pages);
+  const int p1 = min(p0 + chunk, pages);
+
+  f16x2 qv[G][DPL / 2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const f16* qp = q + ((size_t)b * H + h0 + g) * D + dq * DPL;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      f16x8 x = *reinterpret_cast<const f16x8*>(qp + 8 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qv[g][4 * i + e] = f16x2{x[2 * e], x[2 * e + 1]};
+    }
+  }
+
+  float m[G], l[G];
+  float o[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[g][i] = 0.f;
+  }
+
+  const int32_t* pt = page_table + (size_t)b * max_pages;
+  for (int p = p0 + wave; p < p1; p += kDecWaves) {
+    const int pid = pt[p];
+    if (pid < 0 || pid >= num_pages) { bad = true; continue; }
+    const size_t base = ((size_t)pid * Hkv + hk) * (kPage * D) + (size_t)tok * D + dq * DPL;
+    f16x8 kv[NV], vv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const f16x8*>(vpool + base + 8 * i);
+    const bool live = p * kPage + tok < ctx;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dot = __builtin_amdgcn_fdot2(qv[g][4 * i + e], f16x2{kv[i][2 * e], kv[i][2 * e + 1]}, dot,
+                                       false);
+        }
+      }
+      dot += __shfl_xor(dot, 1, 64);
+      dot += __shfl_xor(dot, 2, 64);
+      const float st = live ? dot * c : -INFINITY;
+      float mp = st;
+      mp = fmaxf(mp, __shfl_xor(mp, 4, 64));
+      mp = fmaxf(mp, __shfl_xor(mp, 8, 64));
+      mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
+      mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+      const float m_new = fmaxf(m[g], mp);   // finite: token p*16 < ctx
+      const float alpha = (m_new == m[g]) ? 1.f : exp2_hw(m[g] - m_new);
+      const float pr = exp2_hw(st - m_new);
+      l[g] = l[g] * alpha + pr;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][8 * i + e] = fmaf(pr, (float)vv[i][e], o[g][8 * i + e] * alpha);
+      }
+      m[g] = m_new;
+    }
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int sh = 4; sh < 64; sh <<= 1) {
+      l[g] += __shfl_xor(l[g], sh, 64);
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) o[g][i] += __shfl_xor(o[g][i], sh, 64);
+    }
+  }
+  if (bad) sh_bad = 1;
+  if (tok == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) sh_o[wave][g][dq * DPL + i] = o[g][i];
+      if (dq == 0) { sh_m[wave][g] = m[g]; sh_l[wave][g] = l[g]; }
+    }
+  }
+  __syncthreads();
+
+  // Thread x merges column x % D of head x / D across the waves.
+  for (int x = tid; x < G * D; x += kDecThreads) {
+    const int g = x / D, d = x % D;
+    float M = sh_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, sh_m[w][g]);
+    float acc = 0.f, z = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const float e = (sh_m[w][g] == -INFINITY) ? 0.f : exp2_hw(sh_m[w][g] - M);
+        acc += e * sh_o[w][g][d];
+        z += e * sh_l[w][g];
+      }
+    }
+    float out = (z > 0.f) ? acc / z : 0.f;
+    float lse = (z > 0.f) ? (M + log2_hw(z)) * kLn2 : -INFINITY;
+    if (sh_bad) { out = NAN; lse = NAN; }
+    const size_t pidx = ((size_t)b * H + h0 + g) * S + s;
+    part_o[pidx * D + d] = out;
+    if (d == 0) part_lse[pidx] = lse;
+  }
+}
+
 // One workgroup of D threads per (b, h): thread d merges column d.
 template <int D>
 __global__ void __launch_bounds__(D)
@@ -201,6 +348,29 @@ static int decode_split(const void* q, const void* k_pool, const void* v_pool,
   if (!part_o || !part_lse) return FA_ERR_NULL_POINTER;
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Grouped KV heads: G query heads per workgroup share each page read. At
+  // D = 128 four heads' state needs 256 VGPRs (one wave per SIMD, too few to
+  // stream HBM), so G stays at 2 there (measured: group-of-4 pools at 507 µs
+  // with G = 2 vs 706 µs with G = 4 and 750 µs with G = 1).
+  const int64_t group = H / Hkv;
+  const int maxg = D == 128 ? 2 : 4;
+  const int G = (group % 4 == 0 && maxg >= 4) ? 4 : (group % 2 == 0 ? 2 : 1);
+  if (G > 1) {
+    const dim3 ggrid((unsigned)num_splits, (unsigned)(H / G), (unsigned)B);
+#define FA_DEC_GROUP(DD, GG)                                                                      \
+  hipLaunchKernelGGL((fa_decode_split_group_kernel<DD, GG>), ggrid, dim3(kDecThreads), 0, s,       \
+                     (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table, ctx_lens, \
+                     part_o, part_lse, (int)H, (int)Hkv, (int)max_pages, (int)num_pages,           \
+                     (int)num_splits, c)
+    if (D == 128) {
+      FA_DEC_GROUP(128, 2);
+    } else {
+      if (G == 4) FA_DEC_GROUP(64, 4); else FA_DEC_GROUP(64, 2);
+    }
+#undef FA_DEC_GROUP
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? FA_OK : -(int)e;
+  }
   dim3 grid((unsigned)num_splits, (unsigned)H, (unsigned)B);
   if (D == 128) {
     hipLaunchKernelGGL((fa_decode_split_kernel<128>), grid, dim3(kDecThreads), 0, s,

@@ -350,13 +350,6 @@ __device__ __forceinline__ void dma_block_or_zero(const char* head, int head_byt
   dma16(make_rsrc(head + done, bytes), dst, off);
 }
 
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] at bits 3:0, vmcnt[5:4] at
-// bits 15:14, expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // ---------------------------------------------------------------------------
 // Split kernel: 4*KSPLIT waves; wave w is row group w % 4 and key slice w / 4.
@@ -503,15 +496,6 @@ fa_fwd_split_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   rb.template finish<WRITE_L>(O + head, L + hv.l);
 }
 
-// f(integral_constant<int, I>) for I = B .. E-1, expanded at compile time
-// (a fixed instruction schedule must not depend on the loop unroller).
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Pipelined kernel: 4*KSPLIT waves; wave w is row group w % 4 and key slice

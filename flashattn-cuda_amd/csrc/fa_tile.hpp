@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fa {
 
 typedef _Float16 f16;
@@ -112,6 +114,24 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t lds, uin
 // own vector-memory loads issued before this point have completed (gfx9
 // encoding: vmcnt bits [3:0] and [15:14] = 0, expcnt 7, lgkmcnt 15).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// f(integral_constant<int, I>) for I = B .. E-1, expanded at compile time
+// (a fixed instruction schedule must not depend on the loop unroller).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] at bits 3:0, vmcnt[5:4] at
+// bits 15:14, expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 // ---------------------------------------------------------------------------
 // LDS tile layouts. A K or V tile is BC rows (keys) x D fp16, row stride 2*D

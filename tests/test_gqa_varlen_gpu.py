@@ -140,3 +140,36 @@ def test_gqa_rejects_bad_head_counts(fa, dev):
     kv = torch.zeros(1, 4, 64, 64, device=dev)
     with pytest.raises(RuntimeError, match="multiple"):
         fa.forward(q, kv, kv)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("H,Hkv", [(8, 4), (8, 2), (12, 2), (6, 2)])
+def test_gqa_decode_group_kernel(fa, dev, D, H, Hkv):
+    """Groups of 2 and 4 query heads per workgroup (and group 3, which uses one
+    head per workgroup) against the decode oracle over repeated pools,
+    including an invalid page id (NaN for that sequence only)."""
+    B = 3
+    rng = np.random.default_rng(H * 10 + Hkv + D)
+    ctx = np.array([5, 160, 700], np.int32)
+    pages = (ctx + 15) // 16
+    table = np.zeros((B, pages.max()), np.int32)
+    perm = rng.permutation(int(pages.sum())).astype(np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    q = rng.standard_normal((B, H, D)).astype(np.float16)
+    kp = rng.standard_normal((int(pages.sum()), Hkv, 16, D)).astype(np.float16)
+    vp = rng.standard_normal((int(pages.sum()), Hkv, 16, D)).astype(np.float16)
+    tq, tkp, tvp, tctx = (torch.from_numpy(x).to(dev) for x in (q, kp, vp, ctx))
+    for splits in (1, 5, 16):
+        O, L = fa.decode_paged(tq, tkp, tvp, torch.from_numpy(table).to(dev), tctx, splits)
+        g = H // Hkv
+        Or, Lr = decode_attention(q, np.repeat(kp, g, axis=1), np.repeat(vp, g, axis=1), table, ctx)
+        assert np.abs(O.float().cpu().numpy() - Or).max() <= 2e-3, f"splits {splits}"
+        assert (np.abs(L.cpu().numpy() - Lr) / np.maximum(np.abs(Lr), 1)).max() <= 1e-4
+    bad = table.copy()
+    bad[1, 2] = 10 ** 6
+    O, L = fa.decode_paged(tq, tkp, tvp, torch.from_numpy(bad).to(dev), tctx, 4)
+    On = O.float().cpu().numpy()
+    assert np.isnan(On[1]).all() and np.isfinite(On[0]).all() and np.isfinite(On[2]).all()
