@@ -197,7 +197,7 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, const f16* __restrict__ dO,
                    const float* __restrict__ NL, const float* __restrict__ Di,
                    float* __restrict__ dK, float* __restrict__ dV, int N, int num_kb, int total,
-                   float c, float scale) {
+                   int group, float c, float scale) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
@@ -228,8 +228,9 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const float* Dh = Di + (size_t)bh * N;
 
   f16x8 kf[KSTEPS], vf[KSTEPS];   // B operands: K^T and V^T of this wave's keys
-  load_row_operand<D>(K + head, N, k0 + 32 * kw, lane, kf);
-  load_row_operand<D>(V + head, N, k0 + 32 * kw, lane, vf);
+  const size_t kv_head = (size_t)(bh / group) * N * D;   // GQA: K/V head of this query head
+  load_row_operand<D>(K + kv_head, N, k0 + 32 * kw, lane, kf);
+  load_row_operand<D>(V + kv_head, N, k0 + 32 * kw, lane, vf);
   f32x16 acc[2][DB];              // [0] = dV^T, [1] = dK^T (unscaled)
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
@@ -359,7 +360,8 @@ __global__ void __launch_bounds__(256 * G)
 fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, const f16* __restrict__ dO,
                  const float* __restrict__ NL, const float* __restrict__ Di,
-                 float* __restrict__ dQ, int N, int num_qb, int total, float c, float scale) {
+                 float* __restrict__ dQ, int N, int num_qb, int total, int group, float c,
+                 float scale) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
@@ -385,8 +387,9 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 
   const size_t head = (size_t)bh * N * D;
   const int head_bytes = N * D * 2;
-  const char* Kh = reinterpret_cast<const char*>(K + head);
-  const char* Vh = reinterpret_cast<const char*>(V + head);
+  const size_t kv_head = (size_t)(bh / group) * N * D;   // GQA: K/V head of this query head
+  const char* Kh = reinterpret_cast<const char*>(K + kv_head);
+  const char* Vh = reinterpret_cast<const char*>(V + kv_head);
 
   f16x8 qf[KSTEPS], gf[KSTEPS];   // B operands: Q^T and dO^T of this wave's queries
   load_row_operand<D>(Q + head, N, q0 + 32 * qw, lane, qf);
@@ -487,6 +490,24 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   if (grp == 0) store_transposed<D>(dQ + head, N, q0 + 32 * qw, lane, acc[0], scale);
 }
 
+// GQA: dK, dV of KV head hk = sum over its `group` query heads of the
+// per-query-head partials (fp32 [B*H, N*D] -> [B*Hkv, N*D]), four floats per
+// thread.
+__global__ void __launch_bounds__(256)
+fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out, int64_t head_elems,
+                        int64_t kv_heads, int group) {
+  const int64_t i4 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // float4 index in out
+  const int64_t n4 = kv_heads * head_elems / 4;
+  if (i4 >= n4) return;
+  const int64_t hk = (i4 * 4) / head_elems;
+  const int64_t e = i4 * 4 - hk * head_elems;
+  const f32x4* src = reinterpret_cast<const f32x4*>(part + (hk * group) * head_elems + e);
+  const int64_t stride4 = head_elems / 4;
+  f32x4 acc = src[0];
+  for (int j = 1; j < group; ++j) acc += src[j * stride4];
+  reinterpret_cast<f32x4*>(out)[i4] = acc;
+}
+
 // Wave groups per workgroup: two where the registers allow two waves per SIMD
 // (the second group takes the other half of every tile, so the grid stays
 // one workgroup per 128 rows and the SIMDs get a second wave to overlap).
@@ -498,7 +519,7 @@ constexpr int kDqGroups = 2;
 template <int D, bool CAUSAL>
 static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
-                             float* ws, int64_t BH, int N, hipStream_t s) {
+                             float* ws, int64_t B, int64_t H, int64_t Hkv, int N, hipStream_t s) {
   const float scale = (float)(1.0 / sqrt((double)D));
   const float c = scale * kLog2e;
   const f16* Q = (const f16*)q;
@@ -506,18 +527,33 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const f16* V = (const f16*)v;
   const f16* O = (const f16*)o;
   const f16* G = (const f16*)dout;
+  const int64_t BH = B * H;
   const int64_t rows = BH * N;
+  const int group = (int)(H / Hkv);
   float* di = ws;
   float* nl = ws + rows;
+  // GQA: per-query-head dK/dV partials in the workspace, summed per KV head.
+  const int64_t part0 = (2 * rows + 3) / 4 * 4;   // 16-byte aligned start of the partials
+  float* dk_q = group == 1 ? dk : ws + part0;
+  float* dv_q = group == 1 ? dv : ws + part0 + rows * D;
   hipLaunchKernelGGL((fa_bwd_di_kernel<D>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, O,
                      G, lse, di, nl, rows);
   const int nb = (N + kBlk - 1) / kBlk;
   const int total = (int)(BH * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
   hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK>), dim3(total), dim3(256 * GK), 0, s, Q, K,
-                     V, G, nl, di, dk, dv, N, nb, total, c, scale);
+                     V, G, nl, di, dk_q, dv_q, N, nb, total, group, c, scale);
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
-                     G, nl, di, dq, N, nb, total, c, scale);
+                     G, nl, di, dq, N, nb, total, group, c, scale);
+  if (group > 1) {
+    const int64_t head_elems = (int64_t)N * D;
+    const int64_t n4 = B * Hkv * head_elems / 4;
+    const dim3 grid((unsigned)((n4 + 255) / 256));
+    hipLaunchKernelGGL(fa_bwd_group_sum_kernel, grid, dim3(256), 0, s, dk_q, dk, head_elems,
+                       B * Hkv, group);
+    hipLaunchKernelGGL(fa_bwd_group_sum_kernel, grid, dim3(256), 0, s, dv_q, dv, head_elems,
+                       B * Hkv, group);
+  }
   return hipGetLastError();
 }
 
@@ -529,22 +565,53 @@ extern "C" int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N) {
   return 2 * B * H * N;   // D_i, then -L log2(e)
 }
 
+extern "C" int64_t fa_bwd_gqa_workspace_floats(int64_t B, int64_t H, int64_t H_kv, int64_t N,
+                                               int64_t D) {
+  if (B <= 0 || H <= 0 || N <= 0 || H_kv <= 0 || H % H_kv != 0) return 0;
+  // D_i and -L log2(e), then (GQA only, from a 16-byte boundary) the
+  // per-query-head dK and dV partials
+  if (H_kv == H) return 2 * B * H * N;
+  return (2 * B * H * N + 3) / 4 * 4 + 2 * B * H * N * D;
+}
+
+namespace fa {
+namespace bwd {
+static int bwd_run(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                   const float* lse, float* dq, float* dk, float* dv, float* workspace, int64_t B,
+                   int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal, void* stream) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (D == 64) {
+    e = causal ? launch_bwd<64, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s)
+               : launch_bwd<64, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s);
+  } else {
+    e = causal ? launch_bwd<128, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s)
+               : launch_bwd<128, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s);
+  }
+  return e == hipSuccess ? FA_OK : -(int)e;
+}
+}  // namespace bwd
+}  // namespace fa
+
 extern "C" int fa_bwd_f16(const void* q, const void* k, const void* v, const void* o,
                           const void* dout, const float* lse, float* dq, float* dk, float* dv,
                           float* workspace, int64_t B, int64_t H, int64_t N, int64_t D, int causal,
                           void* stream) {
-  using namespace fa::bwd;
   const int st = fa_validate_bwd(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, N, D);
   if (st != FA_OK) return st;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t BH = B * H;
-  hipError_t e;
-  if (D == 64) {
-    e = causal ? launch_bwd<64, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s)
-               : launch_bwd<64, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s);
-  } else {
-    e = causal ? launch_bwd<128, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s)
-               : launch_bwd<128, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, BH, (int)N, s);
-  }
-  return e == hipSuccess ? FA_OK : -(int)e;
+  return fa::bwd::bwd_run(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H, N, D, causal,
+                          stream);
+}
+
+extern "C" int fa_bwd_gqa_f16(const void* q, const void* k, const void* v, const void* o,
+                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                              float* workspace, int64_t B, int64_t H, int64_t H_kv, int64_t N,
+                              int64_t D, int causal, void* stream) {
+  int st = fa_validate_bwd(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, N, D);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  // the partials are written and read as 16-byte vectors
+  if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
+  return fa::bwd::bwd_run(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D, causal,
+                          stream);
 }

@@ -166,9 +166,13 @@ std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Ten
   const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
   TORCH_CHECK(D == 64 || D == 128, "Head dimension must be 64 or 128");
   TORCH_CHECK(N > 0, "N must be > 0");
-  TORCH_CHECK(K.sizes() == Q.sizes() && V.sizes() == Q.sizes() && O.sizes() == Q.sizes() &&
-                  dO.sizes() == Q.sizes(),
-              "K, V, O and dO must have the same shape as Q");
+  TORCH_CHECK(O.sizes() == Q.sizes() && dO.sizes() == Q.sizes(),
+              "O and dO must have the same shape as Q");
+  TORCH_CHECK(K.dim() == 4 && V.sizes() == K.sizes() && K.size(0) == B && K.size(2) == N &&
+                  K.size(3) == D,
+              "K and V must have the same shape as Q, or [B, H_kv, N, D] with H a multiple of H_kv");
+  const int64_t Hkv = K.size(1);
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "H must be a positive multiple of K/V's head count");
   TORCH_CHECK(L.numel() == B * H * N, "L must hold B*H*N logsumexp values");
   const auto dev = Q.device();
   TORCH_CHECK(K.device() == dev && V.device() == dev && O.device() == dev && dO.device() == dev &&
@@ -177,21 +181,19 @@ std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Ten
 
   const c10::DeviceGuard guard(dev);
   const int64_t BH = B * H;
-  auto half = [&](const torch::Tensor& t) {
-    return t.to(torch::kHalf).reshape({BH, N, D}).contiguous();
-  };
+  auto half = [&](const torch::Tensor& t) { return t.to(torch::kHalf).contiguous(); };
   auto Qh = half(Q), Kh = half(K), Vh = half(V), Oh = half(O), dOh = half(dO);
   auto Lf = L.to(torch::kFloat).reshape({BH, N}).contiguous();
   auto f32 = Qh.options().dtype(torch::kFloat);
   auto dQ = torch::empty({B, H, N, D}, f32);
-  auto dK = torch::empty({B, H, N, D}, f32);
-  auto dV = torch::empty({B, H, N, D}, f32);
-  auto ws = torch::empty({fa_bwd_workspace_floats(B, H, N)}, f32);
-  const int st = fa_bwd_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), Oh.data_ptr(),
-                            dOh.data_ptr(), Lf.data_ptr<float>(), dQ.data_ptr<float>(),
-                            dK.data_ptr<float>(), dV.data_ptr<float>(), ws.data_ptr<float>(), B, H,
-                            N, D, causal ? 1 : 0, current_stream(Qh));
-  check_status(st, "fa_bwd_f16");
+  auto dK = torch::empty({B, Hkv, N, D}, f32);
+  auto dV = torch::empty({B, Hkv, N, D}, f32);
+  auto ws = torch::empty({fa_bwd_gqa_workspace_floats(B, H, Hkv, N, D)}, f32);
+  const int st = fa_bwd_gqa_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), Oh.data_ptr(),
+                                dOh.data_ptr(), Lf.data_ptr<float>(), dQ.data_ptr<float>(),
+                                dK.data_ptr<float>(), dV.data_ptr<float>(), ws.data_ptr<float>(), B,
+                                H, Hkv, N, D, causal ? 1 : 0, current_stream(Qh));
+  check_status(st, "fa_bwd_gqa_f16");
   return {dQ, dK, dV};
 }
 

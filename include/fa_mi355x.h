@@ -156,6 +156,24 @@ int fa_bwd_f16(const void* q, const void* k, const void* v, const void* o, const
                int64_t B, int64_t H, int64_t N, int64_t D, int causal, void* stream);
 
 /*
+ * Floats of the workspace fa_bwd_gqa_f16 needs: 2*B*H*N for H_kv == H, plus,
+ * for H_kv < H, the per-query-head dK and dV partials (2*B*H*N*D floats from
+ * the next 16-byte boundary). 0 for invalid sizes.
+ */
+int64_t fa_bwd_gqa_workspace_floats(int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D);
+
+/*
+ * fa_bwd_f16 with grouped KV heads: k, v fp16 [B, H_kv, N, D] (H % H_kv == 0,
+ * else FA_ERR_KV_HEADS) and dk, dv fp32 [B, H_kv, N, D], each the sum over the
+ * H / H_kv query heads that share the KV head. With H_kv < H the workspace
+ * must be 16-byte aligned. No reference counterpart.
+ */
+int fa_bwd_gqa_f16(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                   const float* lse, float* dq, float* dk, float* dv, float* workspace,
+                   int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal,
+                   void* stream);
+
+/*
  * Host-only argument check of the decode entry points. No reference
  * counterpart (the reference has no decode path).
  */

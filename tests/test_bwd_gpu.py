@@ -168,3 +168,30 @@ def test_rejects_bad_arguments(fa, dev):
         fa.backward(x, x, x, x, torch.zeros(1, 1, 9, 64, device=dev), L)
     with pytest.raises(RuntimeError, match="B\\*H\\*N"):
         fa.backward(x, x, x, x, x, torch.zeros(1, 1, 7, device=dev))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("H,Hkv,N,causal", [(8, 2, 256, False), (8, 1, 333, True), (6, 3, 129, False),
+                                           (4, 2, 1024, True)])
+def test_gqa_backward(fa, dev, D, H, Hkv, N, causal):
+    """K/V of H_kv heads: dK, dV are the sums over each KV head's query heads of
+    the oracle's gradients for the repeated K/V (no new arithmetic)."""
+    B = 2
+    rng = np.random.default_rng(H * 100 + Hkv + N + D)
+    Q = rng.standard_normal((B, H, N, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, N, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, N, D)).astype(np.float32)
+    G = rng.standard_normal((B, H, N, D)).astype(np.float32)
+    tq, tk, tv, tg = (torch.from_numpy(x).to(dev) for x in (Q, K, V, G))
+    O, L = fa.forward(tq, tk, tv, causal=causal)
+    dQ, dK, dV = fa.backward(tq, tk, tv, O, tg, L, causal=causal)
+    torch.cuda.synchronize()
+    assert dK.shape == (B, Hkv, N, D) and dV.shape == (B, Hkv, N, D) and dQ.shape == (B, H, N, D)
+    g = H // Hkv
+    rQ, rK, rV = naive_attention_backward(half_cast(Q), np.repeat(half_cast(K), g, axis=1),
+                                          np.repeat(half_cast(V), g, axis=1), half_cast(G), causal)
+    rK = rK.reshape(B, Hkv, g, N, D).sum(axis=2)
+    rV = rV.reshape(B, Hkv, g, N, D).sum(axis=2)
+    # sums of g per-head gradients: the absolute budget grows with g
+    _compare([t.cpu().numpy() for t in (dQ, dK, dV)], [rQ, rK, rV], TIGHT_ATOL * g, TIGHT_RTOL,
+             f"GQA H{H} Hkv{Hkv} N{N} D{D} causal={causal}")

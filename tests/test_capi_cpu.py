@@ -235,3 +235,17 @@ def test_gqa_entry_points_reject_before_touching_the_device(capi):
     gqa = args[:7] + [5] + args[7:] + [A, A, A, None, None]
     assert lib.fa_decode_paged_gqa_f16(*gqa) == capi.STATUS["FA_ERR_KV_HEADS"]
     assert lib.fa_status_str(capi.STATUS["FA_ERR_KV_HEADS"]) == b"H must be a positive multiple of H_kv"
+
+
+def test_bwd_gqa_workspace_and_rejections(capi):
+    lib = capi.load()
+    assert lib.fa_bwd_gqa_workspace_floats(2, 8, 8, 4096, 64) == 2 * 2 * 8 * 4096
+    n = 2 * 1 * 3 * 5
+    assert lib.fa_bwd_gqa_workspace_floats(1, 3, 1, 5, 64) == (n + 3) // 4 * 4 + 2 * 3 * 5 * 64
+    assert lib.fa_bwd_gqa_workspace_floats(1, 3, 2, 5, 64) == 0
+    args = list(_bwd(H=8))
+    gqa = args[:12] + [3] + args[12:]          # insert H_kv after H
+    assert lib.fa_bwd_gqa_f16(*gqa, 0, None) == capi.STATUS["FA_ERR_KV_HEADS"]
+    gqa = args[:12] + [2] + args[12:]
+    gqa[9] = A + 4                             # workspace only 4-byte aligned
+    assert lib.fa_bwd_gqa_f16(*gqa, 0, None) == capi.STATUS["FA_ERR_ALIGNMENT"]
