@@ -275,6 +275,15 @@ def bench_widen(fa, torch, dev, reps=5, iters=50):
     ms = median_of(lambda: fa.forward_varlen(qv, kv_, vv, cu, max(lens)), reps, 5, 20, torch)
     fv = sum(4.0 * H * n * n * D for n in lens)
     res["varlen_H8D64_8seqs_total32768"] = {"ms": round(ms, 5), "TFLOPs": round(fv / ms / 1e9, 1)}
+    # bf16 and GQA backward at the headline shape (2.5x the forward's products)
+    gb = torch.randn_like(q)
+    ob, lb = fa.forward_bf16(q, k, v)
+    ms = median_of(lambda: fa.backward_bf16(q, k, v, ob, gb, lb), reps, 3, iters // 2, torch)
+    res["bwd_bf16_B1H8N4096D64"] = {"ms": round(ms, 4), "TFLOPs": round(2.5 * f / ms / 1e9, 1)}
+    oh, lh = fa.forward(qh, kh, vh)
+    gh = gb.half()
+    ms = median_of(lambda: fa.backward(qh, kh, vh, oh, gh, lh), reps, 3, iters // 2, torch)
+    res["bwd_gqa_H8_Hkv2_N4096D64"] = {"ms": round(ms, 4), "TFLOPs": round(2.5 * f / ms / 1e9, 1)}
     return res
 
 

@@ -86,6 +86,12 @@ def backward(Q, K, V, O, dO, L, causal: bool = False):
     return _C.backward(Q, K, V, O, dO, L, causal)
 
 
+def backward_bf16(Q, K, V, O, dO, L, causal: bool = False):
+    """[dQ, dK, dV] (fp32) of forward_bf16(): inputs in bfloat16, P and dS
+    rounded to bf16 for their products; K/V may have fewer heads (GQA)."""
+    return _C.backward_bf16(Q, K, V, O, dO, L, causal)
+
+
 def kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens=None):
     """Write k_new/v_new [B,H,T,D] into the pools at start_pos[b] + t, in place.
 

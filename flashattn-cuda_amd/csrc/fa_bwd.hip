@@ -130,7 +130,7 @@ __device__ __forceinline__ void store_transposed(float* out, int n, int row0, in
 // (so that P = exp2(S c + NL) takes one fma). 8 lanes per row, one 16-byte
 // chunk each per step (coalesced 128-byte runs), reduced with xor shuffles.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool BF16>
 __global__ void __launch_bounds__(256)
 fa_bwd_di_kernel(const f16* __restrict__ O, const f16* __restrict__ dO,
                  const float* __restrict__ L, float* __restrict__ Di, float* __restrict__ NL,
@@ -144,8 +144,14 @@ fa_bwd_di_kernel(const f16* __restrict__ O, const f16* __restrict__ dO,
 #pragma unroll
     for (int i = part; i < D / 8; i += 8) {
       const f16x8 a = o[i], b = g[i];
+      if constexpr (BF16) {
+        const bf16x8 ab = __builtin_bit_cast(bf16x8, a), bb = __builtin_bit_cast(bf16x8, b);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)b[e], acc);
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)ab[e], (float)bb[e], acc);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)a[e], (float)b[e], acc);
+      }
     }
   }
   acc += __shfl_xor(acc, 1, 8);
@@ -191,7 +197,7 @@ __device__ __forceinline__ void group_reduce(char* smem, int grp, int slot, int 
 // stream through 2 LDS stages; each stage holds Q and dO twice (row swizzle,
 // transposed swizzle) and 64 floats each of NL and D_i.
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, int G>
+template <int D, bool CAUSAL, int G, bool BF16>
 __global__ void __launch_bounds__(256 * G)
 fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, const f16* __restrict__ dO,
@@ -277,8 +283,8 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     f32x16 s = {}, dp = {};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
-      s = mfma32(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
-      dp = mfma32(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
+      s = mma32<BF16>(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
+      dp = mma32<BF16>(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
     }
     mid();
     f32x16 p, g;
@@ -305,12 +311,12 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int j = 2 * qb + h;
-      const f16x8 pb = pack_p(p, h);
-      const f16x8 gb = pack_p(g, h);
+      const f16x8 pb = pack_px<BF16>(p, h);
+      const f16x8 gb = pack_px<BF16>(g, h);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        acc[0][db] = mfma32(load_v_frag<D>(gv, j, db, lane), pb, acc[0][db]);
-        acc[1][db] = mfma32(load_v_frag<D>(qv, j, db, lane), gb, acc[1][db]);
+        acc[0][db] = mma32<BF16>(load_v_frag<D>(gv, j, db, lane), pb, acc[0][db]);
+        acc[1][db] = mma32<BF16>(load_v_frag<D>(qv, j, db, lane), gb, acc[1][db]);
       }
     }
   };
@@ -355,7 +361,7 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // 64 rows stream through 2 LDS stages, each holding K twice (row swizzle,
 // transposed swizzle) and V once (row swizzle).
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, int G>
+template <int D, bool CAUSAL, int G, bool BF16>
 __global__ void __launch_bounds__(256 * G)
 fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, const f16* __restrict__ dO,
@@ -434,8 +440,8 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     f32x16 s = {}, dp = {};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
-      s = mfma32(load_k_frag<D>(kk_t, half, kk, lane), qf[kk], s);
-      dp = mfma32(load_k_frag<D>(vk_t, half, kk, lane), gf[kk], dp);
+      s = mma32<BF16>(load_k_frag<D>(kk_t, half, kk, lane), qf[kk], s);
+      dp = mma32<BF16>(load_k_frag<D>(vk_t, half, kk, lane), gf[kk], dp);
     }
     mid();
     f32x16 p;
@@ -454,10 +460,10 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int j = 2 * half + h;
-      const f16x8 gb = pack_p(g, h);
+      const f16x8 gb = pack_px<BF16>(g, h);
 #pragma unroll
       for (int db = 0; db < DB; ++db)
-        acc[0][db] = mfma32(load_v_frag<D>(kv_t, j, db, lane), gb, acc[0][db]);
+        acc[0][db] = mma32<BF16>(load_v_frag<D>(kv_t, j, db, lane), gb, acc[0][db]);
     }
   };
 
@@ -516,7 +522,7 @@ constexpr int kDkdvGroups = D == 64 ? 2 : 1;
 template <int D>
 constexpr int kDqGroups = 2;
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool BF16>
 static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
                              float* ws, int64_t B, int64_t H, int64_t Hkv, int N, hipStream_t s) {
@@ -536,14 +542,14 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const int64_t part0 = (2 * rows + 3) / 4 * 4;   // 16-byte aligned start of the partials
   float* dk_q = group == 1 ? dk : ws + part0;
   float* dv_q = group == 1 ? dv : ws + part0 + rows * D;
-  hipLaunchKernelGGL((fa_bwd_di_kernel<D>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, O,
+  hipLaunchKernelGGL((fa_bwd_di_kernel<D, BF16>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, O,
                      G, lse, di, nl, rows);
   const int nb = (N + kBlk - 1) / kBlk;
   const int total = (int)(BH * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
-  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK>), dim3(total), dim3(256 * GK), 0, s, Q, K,
+  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
                      V, G, nl, di, dk_q, dv_q, N, nb, total, group, c, scale);
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ, BF16>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
                      G, nl, di, dq, N, nb, total, group, c, scale);
   if (group > 1) {
     const int64_t head_elems = (int64_t)N * D;
@@ -576,19 +582,36 @@ extern "C" int64_t fa_bwd_gqa_workspace_floats(int64_t B, int64_t H, int64_t H_k
 
 namespace fa {
 namespace bwd {
+template <bool BF16>
 static int bwd_run(const void* q, const void* k, const void* v, const void* o, const void* dout,
                    const float* lse, float* dq, float* dk, float* dv, float* workspace, int64_t B,
                    int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal, void* stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int n = (int)N;
   hipError_t e;
   if (D == 64) {
-    e = causal ? launch_bwd<64, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s)
-               : launch_bwd<64, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s);
+    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s)
+               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s);
   } else {
-    e = causal ? launch_bwd<128, true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s)
-               : launch_bwd<128, false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, (int)N, s);
+    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s)
+               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s);
   }
   return e == hipSuccess ? FA_OK : -(int)e;
+}
+
+static int bwd_gqa(bool bf16, const void* q, const void* k, const void* v, const void* o,
+                   const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                   float* workspace, int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D,
+                   int causal, void* stream) {
+  int st = fa_validate_bwd(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, N, D);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  // the partials are written and read as 16-byte vectors
+  if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
+  return bf16 ? bwd_run<true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
+                              causal, stream)
+              : bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
+                               causal, stream);
 }
 }  // namespace bwd
 }  // namespace fa
@@ -597,21 +620,22 @@ extern "C" int fa_bwd_f16(const void* q, const void* k, const void* v, const voi
                           const void* dout, const float* lse, float* dq, float* dk, float* dv,
                           float* workspace, int64_t B, int64_t H, int64_t N, int64_t D, int causal,
                           void* stream) {
-  const int st = fa_validate_bwd(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, N, D);
-  if (st != FA_OK) return st;
-  return fa::bwd::bwd_run(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H, N, D, causal,
-                          stream);
+  return fa::bwd::bwd_gqa(false, q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H, N, D,
+                          causal, stream);
 }
 
 extern "C" int fa_bwd_gqa_f16(const void* q, const void* k, const void* v, const void* o,
                               const void* dout, const float* lse, float* dq, float* dk, float* dv,
                               float* workspace, int64_t B, int64_t H, int64_t H_kv, int64_t N,
                               int64_t D, int causal, void* stream) {
-  int st = fa_validate_bwd(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, N, D);
-  if (st != FA_OK) return st;
-  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
-  // the partials are written and read as 16-byte vectors
-  if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
-  return fa::bwd::bwd_run(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D, causal,
-                          stream);
+  return fa::bwd::bwd_gqa(false, q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
+                          causal, stream);
+}
+
+extern "C" int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* o,
+                           const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                           float* workspace, int64_t B, int64_t H, int64_t H_kv, int64_t N,
+                           int64_t D, int causal, void* stream) {
+  return fa::bwd::bwd_gqa(true, q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
+                          causal, stream);
 }

@@ -284,4 +284,16 @@ __device__ __forceinline__ f16x8 pack_p(const f32x16& p, int half_sel) {
   return f16x8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
 }
 
+// pack_p with the operand format chosen by BF16 (bfloat16 bits in the same
+// register layout).
+template <bool BF16>
+__device__ __forceinline__ f16x8 pack_px(const f32x16& p, int half_sel) {
+  const int b = 8 * half_sel;
+  f16x2 x0 = cvt2x<BF16>(p[b + 0], p[b + 1]);
+  f16x2 x1 = cvt2x<BF16>(p[b + 2], p[b + 3]);
+  f16x2 x2 = cvt2x<BF16>(p[b + 4], p[b + 5]);
+  f16x2 x3 = cvt2x<BF16>(p[b + 6], p[b + 7]);
+  return f16x8{x0[0], x0[1], x1[0], x1[1], x2[0], x2[1], x3[0], x3[1]};
+}
+
 }  // namespace fa

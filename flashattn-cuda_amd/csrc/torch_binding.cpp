@@ -155,9 +155,10 @@ std::vector<torch::Tensor> forward_varlen(torch::Tensor q, torch::Tensor k, torc
 // function of cuda/flash_attn_kernel.cu:417-503 (checks :425-432). Q/K/V/O/dO
 // are cast to fp16 (O from forward() already is), L to fp32; the D_i
 // workspace comes from the caching allocator.
-std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
-                                    torch::Tensor O, torch::Tensor dO, torch::Tensor L,
-                                    bool causal) {
+static std::vector<torch::Tensor> backward_impl(torch::Tensor Q, torch::Tensor K,
+                                                torch::Tensor V, torch::Tensor O,
+                                                torch::Tensor dO, torch::Tensor L, bool causal,
+                                                bool bf16) {
   TORCH_CHECK(Q.is_cuda(), "Q must be a CUDA tensor");
   TORCH_CHECK(dO.is_cuda(), "dO must be a CUDA tensor");
   TORCH_CHECK(K.is_cuda() && V.is_cuda() && O.is_cuda() && L.is_cuda(),
@@ -181,7 +182,8 @@ std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Ten
 
   const c10::DeviceGuard guard(dev);
   const int64_t BH = B * H;
-  auto half = [&](const torch::Tensor& t) { return t.to(torch::kHalf).contiguous(); };
+  const auto in_type = bf16 ? torch::kBFloat16 : torch::kHalf;
+  auto half = [&](const torch::Tensor& t) { return t.to(in_type).contiguous(); };
   auto Qh = half(Q), Kh = half(K), Vh = half(V), Oh = half(O), dOh = half(dO);
   auto Lf = L.to(torch::kFloat).reshape({BH, N}).contiguous();
   auto f32 = Qh.options().dtype(torch::kFloat);
@@ -189,12 +191,27 @@ std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Ten
   auto dK = torch::empty({B, Hkv, N, D}, f32);
   auto dV = torch::empty({B, Hkv, N, D}, f32);
   auto ws = torch::empty({fa_bwd_gqa_workspace_floats(B, H, Hkv, N, D)}, f32);
-  const int st = fa_bwd_gqa_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), Oh.data_ptr(),
-                                dOh.data_ptr(), Lf.data_ptr<float>(), dQ.data_ptr<float>(),
-                                dK.data_ptr<float>(), dV.data_ptr<float>(), ws.data_ptr<float>(), B,
-                                H, Hkv, N, D, causal ? 1 : 0, current_stream(Qh));
-  check_status(st, "fa_bwd_gqa_f16");
+  auto entry = bf16 ? fa_bwd_bf16 : fa_bwd_gqa_f16;
+  const int st = entry(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), Oh.data_ptr(), dOh.data_ptr(),
+                       Lf.data_ptr<float>(), dQ.data_ptr<float>(), dK.data_ptr<float>(),
+                       dV.data_ptr<float>(), ws.data_ptr<float>(), B, H, Hkv, N, D,
+                       causal ? 1 : 0, current_stream(Qh));
+  check_status(st, bf16 ? "fa_bwd_bf16" : "fa_bwd_gqa_f16");
   return {dQ, dK, dV};
+}
+
+std::vector<torch::Tensor> backward(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                    torch::Tensor O, torch::Tensor dO, torch::Tensor L,
+                                    bool causal) {
+  return backward_impl(Q, K, V, O, dO, L, causal, /*bf16=*/false);
+}
+
+// backward_bf16(Q, K, V, O, dO, L, causal=False) -> [dQ, dK, dV] float32: the
+// backward of forward_bf16 (inputs cast to bf16). No reference counterpart.
+std::vector<torch::Tensor> backward_bf16(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                         torch::Tensor O, torch::Tensor dO, torch::Tensor L,
+                                         bool causal) {
+  return backward_impl(Q, K, V, O, dO, L, causal, /*bf16=*/true);
 }
 
 // Test support: the forward through one explicit kernel variant.
@@ -442,6 +459,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("k"), py::arg("v"), py::arg("cu_seqlens"), py::arg("max_seqlen"),
         py::arg("causal") = false);
   m.def("backward", &backward, "FlashAttention backward: returns [dQ, dK, dV] float",
+        py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("dO"), py::arg("L"),
+        py::arg("causal") = false);
+  m.def("backward_bf16", &backward_bf16, "bfloat16 backward: returns [dQ, dK, dV] float",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("dO"), py::arg("L"),
         py::arg("causal") = false);
   m.def("kv_append", &kv_append, "write new K/V rows into the paged pools; returns bad [B]",

@@ -174,6 +174,17 @@ int fa_bwd_gqa_f16(const void* q, const void* k, const void* v, const void* o, c
                    void* stream);
 
 /*
+ * bfloat16 backward: fa_bwd_gqa_f16 with q, k, v, o, dout in bf16 (H_kv == H
+ * for plain multi-head); P and dS are rounded to bf16 for their products,
+ * everything else as in the fp16 path. Workspace: fa_bwd_gqa_workspace_floats.
+ * No reference counterpart.
+ */
+int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                const float* lse, float* dq, float* dk, float* dv, float* workspace,
+                int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal,
+                void* stream);
+
+/*
  * Host-only argument check of the decode entry points. No reference
  * counterpart (the reference has no decode path).
  */

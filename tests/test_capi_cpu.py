@@ -249,3 +249,9 @@ def test_bwd_gqa_workspace_and_rejections(capi):
     gqa = args[:12] + [2] + args[12:]
     gqa[9] = A + 4                             # workspace only 4-byte aligned
     assert lib.fa_bwd_gqa_f16(*gqa, 0, None) == capi.STATUS["FA_ERR_ALIGNMENT"]
+    # the bf16 backward shares the checks
+    assert lib.fa_bwd_bf16(*gqa, 0, None) == capi.STATUS["FA_ERR_ALIGNMENT"]
+    gqa = args[:12] + [3] + args[12:]
+    assert lib.fa_bwd_bf16(*gqa, 0, None) == capi.STATUS["FA_ERR_KV_HEADS"]
+    gqa[0] = None
+    assert lib.fa_bwd_bf16(*gqa, 0, None) == capi.STATUS["FA_ERR_NULL_POINTER"]
