@@ -39,6 +39,10 @@ def kernel_name(variant, D, causal=False, write_l=True, full=True):
     c, w, f = (str(x).lower() for x in (causal, write_l, full))
     if variant == 204:
         return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4>"
+    if variant == 308:
+        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},8,false,4>"
+    if variant == 404:
+        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4,false,2,2>"
     if variant > 100:
         return f"fa_fwd_pipe_kernel<{D},{c},{w},{f},{variant % 10},{(variant - 100) // 10}>"
     return f"fa_fwd_split_kernel<{D},{c},{w},{f},{variant // 10},{variant % 10}>"

@@ -809,24 +809,37 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // RING/2 - 1 steps to land. Tiles past the end are copied with an empty
 // buffer range (zeros).
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false>
-__global__ void __launch_bounds__(512)
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false, int TG = 2,
+          int SUB = 1>
+__global__ void __launch_bounds__(256 * TG)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
                  float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
-  constexpr int TPS = 2;                       // tiles per step (one per group)
-  static_assert(RING == 4 || RING == 6, "an even ring of four or six tiles");
-  constexpr int TILE = kBC * D * 2;
+  // The unit of the ring and of a phase is a tile of SUB * 64 keys: SUB
+  // consecutive 64-key key tiles ("sub-tiles", the unit of masking and of the
+  // copies' bounds), NB 32-key blocks.
+  constexpr int TPS = TG;                      // tiles per step (one per group)
+  constexpr int WAVES = kRowGroups * TG;
+  static_assert(TG == 2 || TG == 4, "two or four tile groups");
+  static_assert(SUB == 1 || SUB == 2, "tiles of 64 or 128 keys");
+  static_assert(RING % TPS == 0 && RING >= 2 * TPS, "a ring of whole steps, two at least");
+  constexpr int NB = 2 * SUB;                  // 32-key blocks per tile
+  constexpr int STILE = kBC * D * 2;           // bytes of a 64-key sub-tile
+  constexpr int TILE = SUB * STILE;
+  constexpr int SBLOCKS = STILE / 1024;        // 1 KiB blocks per sub-tile
   constexpr int BLOCKS = TILE / 1024;          // 1 KiB blocks per tile
   constexpr int LOADS = BLOCKS / 4;            // blocks per M-phase wave per tile
   static_assert(2 * RING * TILE <= 160 * 1024, "slots exceed the 160 KiB LDS");
   using RB = RowBlock<D, CAUSAL, FULL, BF16>;
   constexpr int DB = RB::DB;
   constexpr int KSTEPS = D / 16;
-  constexpr int NMM = D / 8;                   // MFMAs of one QK (= of one PV)
-  constexpr int PF = D == 64 ? 8 : 4;          // operand prefetch distance, in MFMAs
+  constexpr int NMM = NB * KSTEPS;             // MFMAs of one QK (= of one PV)
+  constexpr int PF = (D == 64 && TG == 2) ? 8 : 4;   // operand prefetch distance, in MFMAs
+  // With four groups the M phase runs its PV before its QK, so the scores
+  // can take the registers of P (four waves per SIMD have 128 VGPRs each).
+  constexpr bool SEQ = TG == 4;
   constexpr int REC = (2 + 16 * DB) * 64;      // floats per wave record of the merge
-  static_assert(kRowGroups * REC * 4 <= 2 * RING * TILE, "merge area too small");
+  static_assert((TG - 1) * kRowGroups * REC * 4 <= 2 * RING * TILE, "merge area too small");
   // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
   __shared__ __attribute__((aligned(1024))) char smem[2 * RING * TILE];
 
@@ -835,6 +848,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: SGPR
   const int rg = wave & (kRowGroups - 1);
   const int grp = wave >> 2;
+  const int team = grp / (TG / 2);   // team 0 starts in the S phase
   // Tile of group g in step j.
   auto tile_of = [&](int g, int j) { return TPS * j + g; };
 
@@ -856,17 +870,47 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   rb.init(Q + head, head_bytes, lane, q0 + 32 * rg, N, c);
 
   const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
-  const int n_tiles = (kv_end + kBC - 1) / kBC;
+  const int n_sub = (kv_end + kBC - 1) / kBC;          // 64-key sub-tiles
+  const int n_tiles = (n_sub + SUB - 1) / SUB;
   const int n_steps = (n_tiles + TPS - 1) / TPS;   // tiles per group
 
   const uint32_t lds0 = lds_addr(smem);
   // This wave's share of a tile copy in its M phase: blocks rg*LOADS .. +LOADS.
   uint32_t koff[LOADS], voff[LOADS];
 #pragma unroll
-  for (int i = 0; i < LOADS; ++i) dma_offsets<D>(rg * LOADS + i, lane, koff[i], voff[i]);
+  for (int i = 0; i < LOADS; ++i) dma_offsets<D>((rg * LOADS + i) % SBLOCKS, lane, koff[i], voff[i]);
+  // 1 KiB block b of tile t: sub-tile SUB t + b / SBLOCKS, bounded by its own
+  // buffer range (zeros past the end).
+  auto dma_tile_block = [&](bool is_v, int t, int b, uint32_t dst, uint32_t off) {
+    int st = SUB * t + b / SBLOCKS;
+    const char* src = is_v ? Vh : Kh;
+    if constexpr (SUB > 1) {
+      // wave-uniform, but the compiler loses track of it here: keep the
+      // buffer descriptor in SGPRs explicitly
+      st = __builtin_amdgcn_readfirstlane(st);
+      const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+      const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+      const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+      src = reinterpret_cast<const char*>(((uintptr_t)hi << 32) | lo);
+    }
+    dma_block_or_zero<D, FULL>(src, head_bytes, st, st < n_sub, dst, off);
+  };
+  // With four groups the per-lane offsets are recomputed where they are used
+  // (from a lane id the compiler cannot hoist) instead of held in registers.
+  auto lane_now = [&] {
+    int l = lane;
+    if constexpr (TG == 4) asm volatile("" : "+v"(l));
+    return l;
+  };
   auto copy_block = [&](bool is_v, int t, int i) {
     const uint32_t at = lds0 + ((is_v ? RING : 0) + t % RING) * TILE + (rg * LOADS + i) * 1024;
-    dma_block_or_zero<D, FULL>(is_v ? Vh : Kh, head_bytes, t, t < n_tiles, at, is_v ? voff[i] : koff[i]);
+    uint32_t off = is_v ? voff[i] : koff[i];
+    if constexpr (TG == 4) {
+      uint32_t ko, vo;
+      dma_offsets<D>((rg * LOADS + i) % SBLOCKS, lane_now(), ko, vo);
+      off = is_v ? vo : ko;
+    }
+    dma_tile_block(is_v, t, rg * LOADS + i, at, off);
   };
 
   // Per-lane offsets of the operand fragments within a tile.
@@ -876,33 +920,33 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
   for (int db = 0; db < DB; ++db) voffs[db] = v_frag_off<D>(db, lane);
 
-  // Prologue: every wave copies its share (1/8) of K tiles 0 .. RING-2 and
-  // V tiles 0 .. RING-4 (those read before the first M-phase copies land).
+  // Prologue: the waves share the copies of K tiles 0 .. RING-TPS/2-1 and V
+  // tiles 0 .. RING-3 TPS/2-1 (those read before the first M-phase copies
+  // land), 1 KiB block by block.
   {
-    constexpr int PB = BLOCKS / 8;
-    uint32_t ko[PB], vo[PB];
+    constexpr int NK = RING - TPS / 2, NV = RING - 3 * TPS / 2;
+    constexpr int ITEMS = (NK + NV) * BLOCKS;
 #pragma unroll
-    for (int i = 0; i < PB; ++i) dma_offsets<D>(wave * PB + i, lane, ko[i], vo[i]);
-#pragma unroll
-    for (int x = 0; x < RING - 1; ++x) {
-#pragma unroll
-      for (int i = 0; i < PB; ++i)
-        dma_block_or_zero<D, FULL>(Kh, head_bytes, x, x < n_tiles,
-                                   lds0 + x * TILE + (wave * PB + i) * 1024, ko[i]);
-    }
-#pragma unroll
-    for (int x = 0; x < RING - 3; ++x) {
-#pragma unroll
-      for (int i = 0; i < PB; ++i)
-        dma_block_or_zero<D, FULL>(Vh, head_bytes, x, x < n_tiles,
-                                   lds0 + (RING + x) * TILE + (wave * PB + i) * 1024, vo[i]);
+    for (int it0 = 0; it0 < ITEMS; it0 += WAVES) {
+      const int it = it0 + wave;
+      if (ITEMS % WAVES == 0 || it < ITEMS) {
+        const bool is_v = it >= NK * BLOCKS;
+        const int x = (is_v ? it - NK * BLOCKS : it) / BLOCKS;
+        const int blk = it % BLOCKS;
+        uint32_t ko, vo;
+        dma_offsets<D>(blk % SBLOCKS, lane, ko, vo);
+        dma_tile_block(is_v, x, blk, lds0 + ((is_v ? RING : 0) + x) * TILE + blk * 1024,
+                       is_v ? vo : ko);
+      }
     }
   }
   wait_vmem();
   __syncthreads();
 
-  f32x16 s[2];    // scores of this wave's current tile
-  f16x8 p[4];     // its packed P
+  f32x16 s[NB];       // scores of this wave's current tile
+  f16x8 p[2 * NB];     // its packed P (one per PV k-step)
+  // The two blocks of sub-tile u.
+  auto sub_s = [&](int u) -> f32x16(&)[2] { return *reinterpret_cast<f32x16(*)[2]>(&s[2 * u]); };
 
   using BT = std::true_type;
   using BF = std::false_type;
@@ -918,31 +962,38 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     uint32_t vt = lds0 + (RING + tv % RING) * TILE;
     asm("" : "+s"(kt), "+s"(vt));
     lds_cp kl[KSTEPS], vl[DB];
+    const int ln = lane_now();
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) kl[kk] = lds_lane_base(kt + koffs[kk]);
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      kl[kk] = lds_lane_base(kt + (TG == 4 ? k_frag_off<D>(kk, ln) : koffs[kk]));
 #pragma unroll
-    for (int db = 0; db < DB; ++db) vl[db] = lds_lane_base(vt + voffs[db]);
-    // MFMA m: with PV, even m = PV i, odd m = QK i (i = m / 2); else QK m.
-    // QK i: block i % 2, k-step i / 2. PV i: k-step i / DB, d-block i % DB.
+    for (int db = 0; db < DB; ++db)
+      vl[db] = lds_lane_base(vt + (TG == 4 ? v_frag_off<D>(db, ln) : voffs[db]));
+    // MFMA m is PV i or QK i: with PV and interleaved, even m = PV m / 2 and
+    // odd m = QK m / 2; with PV and SEQ, m < NMM = PV m, else QK m - NMM;
+    // without PV, QK m. QK i: block i % NB, k-step i / NB. PV i: k-step
+    // i / DB, d-block i % DB.
+    auto is_pv = [](int m) { return PV && (SEQ ? m < NMM : (m & 1) == 0); };
+    auto idx = [](int m) { return !PV ? m : (SEQ ? (m < NMM ? m : m - NMM) : m >> 1); };
     auto fetch = [&](int m) -> f16x8 {
-      const int i = PV ? m >> 1 : m;
-      if (PV && (m & 1) == 0) return v_frag_lds<D>(vl[i % DB] + (i / DB) * 16 * 2 * D);
-      return lds_b128(kl[i / 2] + (i % 2) * 32 * 2 * D);
+      const int i = idx(m);
+      if (is_pv(m)) return v_frag_lds<D>(vl[i % DB] + (i / DB) * 16 * 2 * D);
+      return lds_b128(kl[i / NB] + (i % NB) * 32 * 2 * D);
     };
     f16x8 op[NM];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) s[b] = f32x16{};
 #pragma unroll
     for (int m = 0; m < PF; ++m) op[m] = fetch(m);
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NM>([&](auto mi) {
       constexpr int m = decltype(mi)::value;
       if constexpr (m + PF < NM) op[m + PF] = fetch(m + PF);
-      constexpr int i = PV ? m >> 1 : m;
-      if constexpr (PV && (m & 1) == 0) {
+      constexpr int i = idx(m);
+      if constexpr (is_pv(m)) {
         rb.o[i % DB] = mma32<BF16>(op[m], p[i / DB], rb.o[i % DB]);
+      } else if constexpr (i < NB) {
+        s[i % NB] = mma32<BF16>(op[m], rb.qf[i / NB], f32x16{});   // first k-step
       } else {
-        s[i % 2] = mma32<BF16>(op[m], rb.qf[i / 2], s[i % 2]);
+        s[i % NB] = mma32<BF16>(op[m], rb.qf[i / NB], s[i % NB]);
       }
       // Copy c of this phase after MFMA (c + 1) * NM / (NC + 1).
       static_for<0, NC>([&](auto ci) {
@@ -956,13 +1007,22 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // S phase: softmax of tile t (scores in s) into p, the exponentials of a
   // value pair consumed two pairs later.
   auto sphase = [&](int t) {
-    rb.template mask<2>(t, 0, s);
+    if (TG * SUB > 2 && t >= n_tiles) {
+      // a group's last tile can lie past the end: no keys, P = 0
+#pragma unroll
+      for (int j = 0; j < 2 * NB; ++j) p[j] = f16x8{};
+      wait_vmcnt<(RING / TPS - 2) * 2 * LOADS>();
+      return;
+    }
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) rb.template mask<2>(SUB * t + u, 0, sub_s(u));
     const float m_cur = rb.m_run;
-    float ex[16][2];
+    constexpr int PAIRS = 8 * NB;
+    float ex[PAIRS][2];
     float acc[2];
     auto slot = [&](auto ui) {
       constexpr int u = decltype(ui)::value;
-      if constexpr (u < 16) {
+      if constexpr (u < PAIRS) {
         constexpr int b = u / 8, r = 2 * (u % 8);
         ex[u][0] = exp2_hw(fmaf(s[b][r], c, -m_cur));
         ex[u][1] = exp2_hw(fmaf(s[b][r + 1], c, -m_cur));
@@ -979,9 +1039,9 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
         p[2 * b + h][2 * q + 1] = x[1];
       }
     };
-    static_for<0, 18>(slot);
+    static_for<0, PAIRS + 2>(slot);
     float rs = acc[0] + acc[1];
-    if (__builtin_expect(!__all(rs <= kSumLimit), 0)) rs = rb.template rescue<2>(s, p);
+    if (__builtin_expect(!__all(rs <= kSumLimit), 0)) rs = rb.template rescue<NB>(s, p);
     rb.l_run += rs;
     // This wave's copies of its M phase RING/2 - 1 phases of its own back;
     // those of the later M phases stay in flight.
@@ -992,63 +1052,74 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // may otherwise move a softmax across the barrier into the other group's
   // matrix phase. The empty volatile asm ties the scores to a point after the
   // barrier and P to a point before the next one.
-  auto pin_s = [&] { asm volatile("" : "+v"(s[0]), "+v"(s[1])); };
-  auto pin_p = [&] { asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3])); };
+  auto pin_s = [&] {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) asm volatile("" : "+v"(s[b]));
+  };
+  auto pin_p = [&] {
+#pragma unroll
+    for (int j = 0; j < 2 * NB; ++j) asm volatile("" : "+v"(p[j]));
+  };
   // M phase copies: K and V of the tiles RING - TPS after the ones it reads.
   auto mstep = [&](auto with_pv, int tq, int tv) {
     mphase(with_pv, tq, tv, tq + RING - TPS, tv + RING - TPS);
   };
-  if (grp == 0) {
-    rb.template qk<2>(smem + (tile_of(0, 0) % RING) * TILE, 0, s);
+  if (team == 0) {
+    rb.template qk<NB>(smem + (tile_of(grp, 0) % RING) * TILE, 0, s);
     __syncthreads();                 // its slot is refilled in phase 1
     for (int j = 0; j < n_steps; ++j) {
       pin_s();
-      sphase(tile_of(0, j));
+      sphase(tile_of(grp, j));
       pin_p();
       __syncthreads();
-      mstep(BT{}, tile_of(0, j + 1), tile_of(0, j));
+      mstep(BT{}, tile_of(grp, j + 1), tile_of(grp, j));
       __syncthreads();
     }
-    __syncthreads();   // group 1's last PV
+    __syncthreads();   // team 1's last PV
   } else {
     __syncthreads();
     // Step 0 (no PV yet) is peeled: with both M-phase forms in one loop body
     // the compiler moved the accumulators between them on every step.
-    mstep(BF{}, tile_of(1, 0), tile_of(1, -1));
+    mstep(BF{}, tile_of(grp, 0), tile_of(grp, -1));
     __syncthreads();
     pin_s();
-    sphase(tile_of(1, 0));
+    sphase(tile_of(grp, 0));
     pin_p();
     __syncthreads();
     for (int j = 1; j < n_steps; ++j) {
-      mstep(BT{}, tile_of(1, j), tile_of(1, j - 1));
+      mstep(BT{}, tile_of(grp, j), tile_of(grp, j - 1));
       __syncthreads();
       pin_s();
-      sphase(tile_of(1, j));
+      sphase(tile_of(grp, j));
       pin_p();
       __syncthreads();
     }
     // Phase 2n: the last PV.
-    rb.template pv<2>(smem + (RING + tile_of(1, n_steps - 1) % RING) * TILE, 0, p);
+    rb.template pv<NB>(smem + (RING + tile_of(grp, n_steps - 1) % RING) * TILE, 0, p);
     __syncthreads();
   }
   wait_vmem();   // copies of the last M phases
 
-  // Merge group 1 into group 0 through LDS (the ring is free: all copies
-  // have landed and every read is done).
-  float* area = reinterpret_cast<float*>(smem) + rg * REC;
+  // Merge groups 1 .. TG-1 into group 0 through LDS (the ring is free: all
+  // copies have landed and every read is done).
+  float* area = reinterpret_cast<float*>(smem) + rg * (TG - 1) * REC;
   __syncthreads();
-  if (grp == 1) rb.save_to(area);
+  if (grp > 0) rb.save_to(area + (grp - 1) * REC);
   __syncthreads();
-  if (grp == 1) return;
-  rb.merge_from(area);
+  if (grp > 0) return;
+#pragma unroll
+  for (int g = 1; g < TG; ++g) rb.merge_from(area + (g - 1) * REC);
   rb.template finish<WRITE_L>(O + head, L + hv.l);
 }
 
 // Kernel variants: 10*k + s = split kernel with KSPLIT k and s LDS stages;
 // 100 + 10*r + k = pipelined kernel with KSPLIT k and a ring of r slots;
-// 200 + r = ping-pong kernel with a ring of r tiles.
+// 200 + r = ping-pong kernel with a ring of r tiles; 300 + r = ping-pong
+// kernel with four tile groups (two wave teams) and a ring of r tiles;
+// 400 + r = ping-pong kernel with 128-key tiles and a ring of r of them.
 constexpr int kPingPong = 204;
+constexpr int kPingPong4 = 308;
+constexpr int kPingPongWide = 404;
 constexpr int pipe_code(int ksplit, int ring) { return 100 + 10 * ring + ksplit; }
 
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int KSPLIT, int STAGES>
@@ -1069,6 +1140,8 @@ static void launch_pipe(const f16* Q, const f16* K, const f16* V, f16* O, float*
 static bool variant_fits(int D, int variant) {
   const int tile = 64 * D * 2;
   if (variant == kPingPong) return true;
+  if (variant == kPingPong4) return D == 64;   // 128 VGPRs per wave hold D = 64 only
+  if (variant == kPingPongWide) return D == 64;   // two 128-key rings exceed the LDS at D = 128
   if (variant > 100) {
     const int ks = variant % 10, ring = (variant - 100) / 10;
     if ((ks != 1 && ks != 2) || ring < 2 || ring > 4) return false;
@@ -1092,6 +1165,21 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
       hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4>), dim3(total), dim3(512), 0,
                          stream, Q, K, V, Op, lse, geo, num_qb, total, c);
       break;
+    case kPingPong4:
+      if constexpr (D == 64) {
+        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, false, 4>), dim3(total),
+                           dim3(1024), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
+        break;
+      }
+      return hipErrorInvalidValue;
+    case kPingPongWide:
+      if constexpr (D == 64) {
+        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4, false, 2, 2>),
+                           dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb,
+                           total, c);
+        break;
+      }
+      return hipErrorInvalidValue;
     case pipe_code(1, 2): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 2>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
     case pipe_code(1, 3): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 3>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
     case pipe_code(1, 4): launch_pipe<D, CAUSAL, WRITE_L, FULL, 1, 4>(Q, K, V, Op, lse, geo, num_qb, total, c, stream); break;
@@ -1131,8 +1219,8 @@ static hipError_t dispatch_wl(const void* q, const void* k, const void* v, void*
 }
 
 // Variant choice (measured on MI355X; see bench.py). The environment
-// variable FA_MI355X_FWD_VARIANT ("pipe<k>r<r>" or "split<k>s<s>", e.g.
-// pipe1r3, split1s4)
+// variable FA_MI355X_FWD_VARIANT ("pingpong", "pingpong4", "pingpongwide",
+// "pipe<k>r<r>" or "split<k>s<s>", e.g. pipe1r3, split1s4)
 // forces one that fits D; it is read once, for measurement and tests.
 static int choose_variant(int64_t D) {
   static const int forced = [] {
@@ -1140,6 +1228,8 @@ static int choose_variant(int64_t D) {
     if (!e) return -1;
     int ks = 0, st = 0;
     if (strcmp(e, "pingpong") == 0) return kPingPong;
+    if (strcmp(e, "pingpong4") == 0) return kPingPong4;
+    if (strcmp(e, "pingpongwide") == 0) return kPingPongWide;
     if (sscanf(e, "pipe%dr%d", &ks, &st) == 2) return pipe_code(ks, st);
     if (sscanf(e, "split%ds%d", &ks, &st) == 2) return 10 * ks + st;
     return -1;
@@ -1275,7 +1365,7 @@ extern "C" int fa_probe_default_variant(int64_t D) {
 }
 
 extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D) {
-  static const int all[] = {12, 13, 14, 22, 23, 24, 42, 121, 131, 141, 122, 132, 204};
+  static const int all[] = {12, 13, 14, 22, 23, 24, 42, 121, 131, 141, 122, 132, 204, 308, 404};
   int n = 0;
   for (int v : all) {
     if (fa::variant_fits((int)D, v)) {
