@@ -279,6 +279,12 @@ def bench_widen(fa, torch, dev, reps=5, iters=50):
     ms = median_of(lambda: fa.forward_varlen(qv, kv_, vv, cu, max(lens)), reps, 5, 20, torch)
     fv = sum(4.0 * H * n * n * D for n in lens)
     res["varlen_H8D64_8seqs_total32768"] = {"ms": round(ms, 5), "TFLOPs": round(fv / ms / 1e9, 1)}
+    ov, lv = fa.forward_varlen(qv, kv_, vv, cu, max(lens))
+    gv = torch.randn_like(qv)
+    ms = median_of(lambda: fa.backward_varlen(qv, kv_, vv, ov, gv, lv, cu, max(lens)), 3, 2, 5,
+                   torch)
+    res["bwd_varlen_H8D64_8seqs_total32768"] = {"ms": round(ms, 4),
+                                                "TFLOPs": round(2.5 * fv / ms / 1e9, 1)}
     # bf16 and GQA backward at the headline shape (2.5x the forward's products)
     gb = torch.randn_like(q)
     ob, lb = fa.forward_bf16(q, k, v)

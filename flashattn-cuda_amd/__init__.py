@@ -92,6 +92,12 @@ def backward_bf16(Q, K, V, O, dO, L, causal: bool = False):
     return _C.backward_bf16(Q, K, V, O, dO, L, causal)
 
 
+def backward_varlen(q, k, v, o, dO, L, cu_seqlens, max_seqlen: int, causal: bool = False):
+    """[dQ, dK, dV] (fp32, head-major packed like forward_varlen's inputs) of
+    forward_varlen(); rows outside every sequence are zeros."""
+    return _C.backward_varlen(q, k, v, o, dO, L, cu_seqlens, max_seqlen, causal)
+
+
 def kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens=None):
     """Write k_new/v_new [B,H,T,D] into the pools at start_pos[b] + t, in place.
 

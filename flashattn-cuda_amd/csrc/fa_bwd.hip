@@ -202,8 +202,8 @@ __global__ void __launch_bounds__(256 * G)
 fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, const f16* __restrict__ dO,
                    const float* __restrict__ NL, const float* __restrict__ Di,
-                   float* __restrict__ dK, float* __restrict__ dV, int N, int num_kb, int total,
-                   int group, float c, float scale) {
+                   float* __restrict__ dK, float* __restrict__ dV, Geom geo, int num_kb,
+                   int total, float c, float scale) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
@@ -226,15 +226,18 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int k0 = kb * kBlk;
   const int key = k0 + 32 * kw + (lane & 31);
 
-  const size_t head = (size_t)bh * N * D;
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (k0 >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
   const int head_bytes = N * D * 2;
   const char* Qh = reinterpret_cast<const char*>(Q + head);
   const char* Gh = reinterpret_cast<const char*>(dO + head);
-  const float* Lh = NL + (size_t)bh * N;
-  const float* Dh = Di + (size_t)bh * N;
+  const float* Lh = NL + hv.l;
+  const float* Dh = Di + hv.l;
 
   f16x8 kf[KSTEPS], vf[KSTEPS];   // B operands: K^T and V^T of this wave's keys
-  const size_t kv_head = (size_t)(bh / group) * N * D;   // GQA: K/V head of this query head
+  const size_t kv_head = hv.kv;   // GQA: K/V head of this query head
   load_row_operand<D>(K + kv_head, N, k0 + 32 * kw, lane, kf);
   load_row_operand<D>(V + kv_head, N, k0 + 32 * kw, lane, vf);
   f32x16 acc[2][DB];              // [0] = dV^T, [1] = dK^T (unscaled)
@@ -366,7 +369,7 @@ __global__ void __launch_bounds__(256 * G)
 fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, const f16* __restrict__ dO,
                  const float* __restrict__ NL, const float* __restrict__ Di,
-                 float* __restrict__ dQ, int N, int num_qb, int total, int group, float c,
+                 float* __restrict__ dQ, Geom geo, int num_qb, int total, float c,
                  float scale) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
@@ -391,9 +394,12 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int q0 = qb * kBlk;
   const int query = q0 + 32 * qw + (lane & 31);
 
-  const size_t head = (size_t)bh * N * D;
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (q0 >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
   const int head_bytes = N * D * 2;
-  const size_t kv_head = (size_t)(bh / group) * N * D;   // GQA: K/V head of this query head
+  const size_t kv_head = hv.kv;   // GQA: K/V head of this query head
   const char* Kh = reinterpret_cast<const char*>(K + kv_head);
   const char* Vh = reinterpret_cast<const char*>(V + kv_head);
 
@@ -401,8 +407,8 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   load_row_operand<D>(Q + head, N, q0 + 32 * qw, lane, qf);
   load_row_operand<D>(dO + head, N, q0 + 32 * qw, lane, gf);
   const bool row_ok = query < N;
-  const float nl = row_ok ? NL[(size_t)bh * N + query] : 0.f;
-  const float dq_i = row_ok ? Di[(size_t)bh * N + query] : 0.f;
+  const float nl = row_ok ? NL[hv.l + query] : 0.f;
+  const float dq_i = row_ok ? Di[hv.l + query] : 0.f;
   f32x16 acc[1][DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[0][db] = f32x16{};
@@ -522,10 +528,15 @@ constexpr int kDkdvGroups = D == 64 ? 2 : 1;
 template <int D>
 constexpr int kDqGroups = 2;
 
+// The three passes (D_i and -L log2 e, dK/dV, dQ) and, with H_kv < H, the
+// group sums. geo is dense (B heads of N rows per head) or varlen (heads of
+// geo.total packed rows; units = B*H (b, h) pairs either way); `rows` is the
+// number of L rows: B*H*N dense, H*total varlen.
 template <int D, bool CAUSAL, bool BF16>
 static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
-                             float* ws, int64_t B, int64_t H, int64_t Hkv, int N, hipStream_t s) {
+                             float* ws, const Geom& geo, int64_t units, int64_t rows,
+                             int64_t out_heads, int64_t head_rows, hipStream_t s) {
   const float scale = (float)(1.0 / sqrt((double)D));
   const float c = scale * kLog2e;
   const f16* Q = (const f16*)q;
@@ -533,9 +544,7 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const f16* V = (const f16*)v;
   const f16* O = (const f16*)o;
   const f16* G = (const f16*)dout;
-  const int64_t BH = B * H;
-  const int64_t rows = BH * N;
-  const int group = (int)(H / Hkv);
+  const int group = geo.group;
   float* di = ws;
   float* nl = ws + rows;
   // GQA: per-query-head dK/dV partials in the workspace, summed per KV head.
@@ -544,21 +553,23 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   float* dv_q = group == 1 ? dv : ws + part0 + rows * D;
   hipLaunchKernelGGL((fa_bwd_di_kernel<D, BF16>), dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, O,
                      G, lse, di, nl, rows);
-  const int nb = (N + kBlk - 1) / kBlk;
-  const int total = (int)(BH * nb);
+  const int nb = (geo.N + kBlk - 1) / kBlk;
+  const int total = (int)(units * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
   hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
-                     V, G, nl, di, dk_q, dv_q, N, nb, total, group, c, scale);
+                     V, G, nl, di, dk_q, dv_q, geo, nb, total, c, scale);
   hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ, BF16>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
-                     G, nl, di, dq, N, nb, total, group, c, scale);
+                     G, nl, di, dq, geo, nb, total, c, scale);
   if (group > 1) {
-    const int64_t head_elems = (int64_t)N * D;
-    const int64_t n4 = B * Hkv * head_elems / 4;
+    // out_heads KV heads of head_rows rows, each the sum of `group`
+    // consecutive query heads' partials
+    const int64_t head_elems = head_rows * D;
+    const int64_t n4 = out_heads * head_elems / 4;
     const dim3 grid((unsigned)((n4 + 255) / 256));
     hipLaunchKernelGGL(fa_bwd_group_sum_kernel, grid, dim3(256), 0, s, dk_q, dk, head_elems,
-                       B * Hkv, group);
+                       out_heads, group);
     hipLaunchKernelGGL(fa_bwd_group_sum_kernel, grid, dim3(256), 0, s, dv_q, dv, head_elems,
-                       B * Hkv, group);
+                       out_heads, group);
   }
   return hipGetLastError();
 }
@@ -584,17 +595,17 @@ namespace fa {
 namespace bwd {
 template <bool BF16>
 static int bwd_run(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                   const float* lse, float* dq, float* dk, float* dv, float* workspace, int64_t B,
-                   int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal, void* stream) {
+                   const float* lse, float* dq, float* dk, float* dv, float* workspace,
+                   const Geom& geo, int64_t units, int64_t rows, int64_t out_heads,
+                   int64_t head_rows, int64_t D, int causal, void* stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int n = (int)N;
   hipError_t e;
   if (D == 64) {
-    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s)
-               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s);
+    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s)
+               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s);
   } else {
-    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s)
-               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, n, s);
+    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s)
+               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s);
   }
   return e == hipSuccess ? FA_OK : -(int)e;
 }
@@ -608,10 +619,11 @@ static int bwd_gqa(bool bf16, const void* q, const void* k, const void* v, const
   if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
   // the partials are written and read as 16-byte vectors
   if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
-  return bf16 ? bwd_run<true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
-                              causal, stream)
-              : bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
-                               causal, stream);
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  return bf16 ? bwd_run<true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
+                              B * H * N, B * H_kv, N, D, causal, stream)
+              : bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
+                               B * H * N, B * H_kv, N, D, causal, stream);
 }
 }  // namespace bwd
 }  // namespace fa
@@ -638,4 +650,19 @@ extern "C" int fa_bwd_bf16(const void* q, const void* k, const void* v, const vo
                            int64_t D, int causal, void* stream) {
   return fa::bwd::bwd_gqa(true, q, k, v, o, dout, lse, dq, dk, dv, workspace, B, H, H_kv, N, D,
                           causal, stream);
+}
+
+extern "C" int fa_bwd_varlen_f16(const void* q, const void* k, const void* v, const void* o,
+                                 const void* dout, const float* lse, float* dq, float* dk,
+                                 float* dv, float* workspace, const int32_t* cu_seqlens,
+                                 int64_t B, int64_t H, int64_t H_kv, int64_t max_seqlen,
+                                 int64_t total, int64_t D, int causal, void* stream) {
+  const int st = fa_validate_bwd_varlen(q, k, v, o, dout, lse, dq, dk, dv, workspace, cu_seqlens,
+                                        B, H, H_kv, max_seqlen, total, D);
+  if (st != FA_OK) return st;
+  if (total == 0) return FA_OK;
+  if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
+  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total};
+  return fa::bwd::bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
+                                 H * total, H_kv, total, D, causal, stream);
 }

@@ -109,6 +109,28 @@ extern "C" int fa_validate_bwd(const void* q, const void* k, const void* v, cons
   return FA_OK;
 }
 
+// Varlen backward (no reference counterpart): the varlen forward's checks on
+// q/k/v/o plus the backward's gradient, L and workspace pointers and the row
+// grid of the D_i pass.
+extern "C" int fa_validate_bwd_varlen(const void* q, const void* k, const void* v, const void* o,
+                                      const void* dout, const float* lse, const float* dq,
+                                      const float* dk, const float* dv, const float* workspace,
+                                      const int32_t* cu_seqlens, int64_t B, int64_t H,
+                                      int64_t H_kv, int64_t max_seqlen, int64_t total,
+                                      int64_t D) {
+  if (!dout || !lse || !dq || !dk || !dv || !workspace) return FA_ERR_NULL_POINTER;
+  const int st = fa_validate_fwd_varlen(q, k, v, o, cu_seqlens, B, H, H_kv, max_seqlen, total, D);
+  if (st != FA_OK) return st;
+  if (!aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return FA_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(lse) & 3u) != 0 ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
+    return FA_ERR_ALIGNMENT;
+  if (H > kMaxGrid / (total > 0 ? total : 1)) return FA_ERR_TOO_LARGE;
+  if ((H * total + 31) / 32 > kMaxGrid) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
 // Decode arguments (no reference counterpart): pool/page-table shapes, the
 // split count and the grid limits of the split pass.
 extern "C" int fa_validate_decode(const void* q, const void* k_pool, const void* v_pool,

@@ -65,47 +65,6 @@ __device__ __forceinline__ int xcd_remap(int g, int total) {
   return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
-// Where the heads of one launch live. Dense: Q/O [B, H, N, D], K/V
-// [B, H/group, N, D], L [B, H, N]. Varlen (cu != nullptr): sequences packed
-// head-major, Q/O [H, total, D], K/V [H/group, total, D], L [H, total];
-// sequence b is rows cu[b] .. cu[b+1] of every head and N is the grid's
-// maximum length. Query head h reads KV head h / group (GQA / MQA).
-struct Geom {
-  const int32_t* cu;
-  int N;
-  int H;
-  int group;
-  int total;
-};
-
-// One (b, h): element offsets of its Q/O and K/V rows, of its L row, and its
-// length. Varlen bounds are clamped into [0, total] and to N, so a malformed
-// cu never moves a head's buffer range outside its own rows.
-struct HeadView {
-  size_t q, kv, l;
-  int n;
-};
-
-template <int D>
-__device__ __forceinline__ HeadView head_view(const Geom& g, int bh) {
-  HeadView v;
-  if (g.cu == nullptr) {
-    v.n = g.N;
-    v.q = (size_t)bh * g.N * D;
-    v.kv = (size_t)(bh / g.group) * g.N * D;
-    v.l = (size_t)bh * g.N;
-  } else {
-    const int b = bh / g.H, h = bh - b * g.H;
-    const int s0 = min(max(g.cu[b], 0), g.total);
-    const int s1 = min(max(g.cu[b + 1], s0), g.total);
-    v.n = min(s1 - s0, g.N);
-    v.q = ((size_t)h * g.total + s0) * D;
-    v.kv = ((size_t)(h / g.group) * g.total + s0) * D;
-    v.l = (size_t)h * g.total + s0;
-  }
-  return v;
-}
-
 // State and tile operations of one wave: 32 query rows, one lane pair per row
 // (lanes l and l^32 hold the two halves of every 32-key block).
 template <int D, bool CAUSAL, bool FULL, bool BF16 = false>

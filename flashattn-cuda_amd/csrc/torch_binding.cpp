@@ -214,6 +214,56 @@ std::vector<torch::Tensor> backward_bf16(torch::Tensor Q, torch::Tensor K, torch
   return backward_impl(Q, K, V, O, dO, L, causal, /*bf16=*/true);
 }
 
+// backward_varlen(q, k, v, o, dO, L, cu_seqlens, max_seqlen, causal=False) ->
+// [dQ, dK, dV] float32: the backward of forward_varlen (head-major packed
+// sequences, dQ [H, total, D], dK/dV [H_kv, total, D]). Rows outside every
+// sequence are zeros. No reference counterpart.
+std::vector<torch::Tensor> backward_varlen(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                           torch::Tensor o, torch::Tensor dO, torch::Tensor L,
+                                           torch::Tensor cu_seqlens, int64_t max_seqlen,
+                                           bool causal) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda() && o.is_cuda() && dO.is_cuda() &&
+                  L.is_cuda() && cu_seqlens.is_cuda(),
+              "q/k/v/o/dO/L/cu_seqlens must be CUDA tensors");
+  TORCH_CHECK(q.dim() == 3, "q must be 3D [H, total, D]");
+  const int64_t H = q.size(0), total = q.size(1), D = q.size(2);
+  TORCH_CHECK(D == 64 || D == 128, "Head dimension must be 64 or 128");
+  TORCH_CHECK(k.dim() == 3 && v.sizes() == k.sizes() && k.size(1) == total && k.size(2) == D,
+              "k and v must be [H_kv, total, D] matching q");
+  TORCH_CHECK(o.sizes() == q.sizes() && dO.sizes() == q.sizes(),
+              "o and dO must have the same shape as q");
+  TORCH_CHECK(L.numel() == H * total, "L must hold H*total logsumexp values");
+  TORCH_CHECK(cu_seqlens.dim() == 1 && cu_seqlens.scalar_type() == torch::kInt &&
+                  cu_seqlens.size(0) >= 2,
+              "cu_seqlens must be int32 [B + 1]");
+  const auto dev = q.device();
+  TORCH_CHECK(k.device() == dev && v.device() == dev && o.device() == dev &&
+                  dO.device() == dev && L.device() == dev && cu_seqlens.device() == dev,
+              "all tensors must be on the same device");
+  const c10::DeviceGuard guard(dev);
+  const int64_t B = cu_seqlens.size(0) - 1, Hkv = k.size(0);
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "H must be a positive multiple of k/v's head count");
+  auto half = [&](const torch::Tensor& t) { return t.to(torch::kHalf).contiguous(); };
+  auto qh = half(q), kh = half(k), vh = half(v), oh = half(o), gh = half(dO);
+  auto Lf = L.to(torch::kFloat).reshape({H, total}).contiguous();
+  auto cu = cu_seqlens.contiguous();
+  auto f32 = qh.options().dtype(torch::kFloat);
+  auto dQ = torch::zeros({H, total, D}, f32);
+  auto dK = torch::zeros({Hkv, total, D}, f32);
+  auto dV = torch::zeros({Hkv, total, D}, f32);
+  const int64_t wsn = fa_bwd_gqa_workspace_floats(1, H, Hkv, total > 0 ? total : 1, D);
+  // zeros: with H_kv < H the group sums also read the partials of rows
+  // outside every sequence
+  auto ws = torch::zeros({wsn}, f32);
+  const int st = fa_bwd_varlen_f16(qh.data_ptr(), kh.data_ptr(), vh.data_ptr(), oh.data_ptr(),
+                                   gh.data_ptr(), Lf.data_ptr<float>(), dQ.data_ptr<float>(),
+                                   dK.data_ptr<float>(), dV.data_ptr<float>(),
+                                   ws.data_ptr<float>(), cu.data_ptr<int32_t>(), B, H, Hkv,
+                                   max_seqlen, total, D, causal ? 1 : 0, current_stream(qh));
+  check_status(st, "fa_bwd_varlen_f16");
+  return {dQ, dK, dV};
+}
+
 // Test support: the forward through one explicit kernel variant.
 std::vector<torch::Tensor> probe_fwd_variant(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                                              bool causal, int64_t variant, bool want_L) {
@@ -464,6 +514,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("backward_bf16", &backward_bf16, "bfloat16 backward: returns [dQ, dK, dV] float",
         py::arg("Q"), py::arg("K"), py::arg("V"), py::arg("O"), py::arg("dO"), py::arg("L"),
         py::arg("causal") = false);
+  m.def("backward_varlen", &backward_varlen,
+        "varlen backward: returns [dQ, dK, dV] float (head-major packed)", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("o"), py::arg("dO"), py::arg("L"),
+        py::arg("cu_seqlens"), py::arg("max_seqlen"), py::arg("causal") = false);
   m.def("kv_append", &kv_append, "write new K/V rows into the paged pools; returns bad [B]",
         py::arg("k_new"), py::arg("v_new"), py::arg("k_pool"), py::arg("v_pool"),
         py::arg("page_table"), py::arg("start_pos"), py::arg("new_lens") = py::none());

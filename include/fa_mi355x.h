@@ -185,6 +185,29 @@ int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* o, cons
                 void* stream);
 
 /*
+ * Backward of fa_fwd_varlen_f16: q/o/dout [H, total, D] fp16, k/v [H_kv,
+ * total, D] fp16, lse [H, total] fp32 (the forward's L), sequence b = rows
+ * cu_seqlens[b] .. cu_seqlens[b+1] of every head (bounds clamped as in the
+ * forward); dq [H, total, D], dk/dv [H_kv, total, D] fp32. Workspace:
+ * fa_bwd_gqa_workspace_floats(1, H, H_kv, total, D) floats, 16-byte aligned
+ * when H_kv < H. Rows outside every sequence are not written (with H_kv < H
+ * dk/dv get the sum of the workspace's unwritten partial rows there: zero
+ * the workspace first where zeros are wanted). No reference counterpart.
+ */
+int fa_bwd_varlen_f16(const void* q, const void* k, const void* v, const void* o,
+                      const void* dout, const float* lse, float* dq, float* dk, float* dv,
+                      float* workspace, const int32_t* cu_seqlens, int64_t B, int64_t H,
+                      int64_t H_kv, int64_t max_seqlen, int64_t total, int64_t D, int causal,
+                      void* stream);
+
+/* Host-only argument check of fa_bwd_varlen_f16. */
+int fa_validate_bwd_varlen(const void* q, const void* k, const void* v, const void* o,
+                           const void* dout, const float* lse, const float* dq, const float* dk,
+                           const float* dv, const float* workspace, const int32_t* cu_seqlens,
+                           int64_t B, int64_t H, int64_t H_kv, int64_t max_seqlen,
+                           int64_t total, int64_t D);
+
+/*
  * Host-only argument check of the decode entry points. No reference
  * counterpart (the reference has no decode path).
  */

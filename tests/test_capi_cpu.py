@@ -255,3 +255,23 @@ def test_bwd_gqa_workspace_and_rejections(capi):
     assert lib.fa_bwd_bf16(*gqa, 0, None) == capi.STATUS["FA_ERR_KV_HEADS"]
     gqa[0] = None
     assert lib.fa_bwd_bf16(*gqa, 0, None) == capi.STATUS["FA_ERR_NULL_POINTER"]
+
+
+def test_validate_bwd_varlen(capi):
+    lib = capi.load()
+    ok = [A] * 11 + [3, 8, 2, 512, 1000, 64]
+    assert lib.fa_validate_bwd_varlen(*ok) == capi.STATUS["FA_OK"]
+    bad = list(ok); bad[10] = None                     # cu_seqlens
+    assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_NULL_POINTER"]
+    bad = list(ok); bad[4] = None                      # dout
+    assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_NULL_POINTER"]
+    bad = list(ok); bad[13] = 3                        # H_kv does not divide H
+    assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_KV_HEADS"]
+    bad = list(ok); bad[16] = 96
+    assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_HEAD_DIM"]
+    bad = list(ok); bad[6] = A + 8                     # dq not 16-byte aligned
+    assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_ALIGNMENT"]
+    bad = list(ok); bad[14] = 0                        # max_seqlen
+    assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_SEQ_LEN"]
+    # the entry point rejects before touching the device
+    assert lib.fa_bwd_varlen_f16(*bad, 0, None) == capi.STATUS["FA_ERR_SEQ_LEN"]

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import decode_attention, half_cast, naive_attention
+from oracle import decode_attention, half_cast, naive_attention, naive_attention_backward
 
 from test_fwd_gpu import _check
 
@@ -173,3 +173,55 @@ def test_gqa_decode_group_kernel(fa, dev, D, H, Hkv):
     O, L = fa.decode_paged(tq, tkp, tvp, torch.from_numpy(bad).to(dev), tctx, 4)
     On = O.float().cpu().numpy()
     assert np.isnan(On[1]).all() and np.isfinite(On[0]).all() and np.isfinite(On[2]).all()
+
+
+# Backward of the packed layout: each sequence against the oracle's backward
+# of that sequence alone (K/V repeated per group, dK/dV summed per KV head),
+# at the dense backward's bound (tests/test_bwd_gpu.py): |g - g_ref| <=
+# 5e-3 + 5e-3 |g_ref|, the absolute part times the group for dK/dV.
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Hkv", [4, 2])
+def test_varlen_backward(fa, dev, D, causal, Hkv):
+    H = 4
+    lengths = [1, 100, 0, 257, 300, 63, 128]
+    cu = _cu(lengths)
+    total = int(cu[-1]) + 5                  # 5 trailing rows outside every sequence
+    q, o_g = _randn((H, total, D), 20), _randn((H, total, D), 23)
+    k, v = _randn((Hkv, total, D), 21), _randn((Hkv, total, D), 22)
+    tq, tk, tv, tg, tcu = (torch.from_numpy(x).to(dev) for x in (q, k, v, o_g, cu))
+    O, L = fa.forward_varlen(tq, tk, tv, tcu, max(lengths), causal=causal)
+    dQ, dK, dV = fa.backward_varlen(tq, tk, tv, O, tg, L, tcu, max(lengths), causal=causal)
+    torch.cuda.synchronize()
+    assert dQ.shape == (H, total, D) and dK.shape == (Hkv, total, D) and dV.shape == dK.shape
+    g = H // Hkv
+    got = [t.cpu().numpy() for t in (dQ, dK, dV)]
+    for b, n in enumerate(lengths):
+        if n == 0:
+            continue
+        s0, s1 = cu[b], cu[b + 1]
+        rQ, rK, rV = naive_attention_backward(
+            half_cast(q[None, :, s0:s1]), np.repeat(half_cast(k[None, :, s0:s1]), g, axis=1),
+            np.repeat(half_cast(v[None, :, s0:s1]), g, axis=1), half_cast(o_g[None, :, s0:s1]),
+            causal)
+        rK = rK.reshape(1, Hkv, g, n, D).sum(axis=2)
+        rV = rV.reshape(1, Hkv, g, n, D).sum(axis=2)
+        for name, x, r, atol in (("dQ", got[0], rQ, 5e-3), ("dK", got[1], rK, 5e-3 * g),
+                                 ("dV", got[2], rV, 5e-3 * g)):
+            err = np.abs(x[None, :, s0:s1] - r)
+            assert (err <= atol + 5e-3 * np.abs(r)).all(), \
+                f"{name} seq {b} (n={n}) D{D} causal={causal} Hkv{Hkv}: max err {err.max():.3e}"
+    for x in got:
+        assert not x[:, cu[-1]:].any(), "rows outside every sequence must stay zero"
+
+
+def test_varlen_backward_single_sequence_matches_dense(fa, dev):
+    H, N, D = 2, 384, 64
+    q, k, v, gr = (torch.from_numpy(_randn((H, N, D), s)).to(dev).half() for s in (30, 31, 32, 33))
+    cu = torch.tensor([0, N], dtype=torch.int32, device=dev)
+    Ov, Lv = fa.forward_varlen(q, k, v, cu, N, causal=True)
+    gv = fa.backward_varlen(q, k, v, Ov, gr, Lv, cu, N, causal=True)
+    Od, Ld = fa.forward(q[None], k[None], v[None], causal=True)
+    gd = fa.backward(q[None], k[None], v[None], Od, gr[None], Ld, causal=True)
+    for a, b in zip(gv, gd):
+        assert (a - b[0]).abs().max().item() <= 1e-3
