@@ -662,7 +662,7 @@ extern "C" int fa_bwd_varlen_f16(const void* q, const void* k, const void* v, co
   if (st != FA_OK) return st;
   if (total == 0) return FA_OK;
   if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
-  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total};
+  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total, (int)B};
   return fa::bwd::bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
                                  H * total, H_kv, total, D, causal, stream);
 }

@@ -1255,7 +1255,7 @@ extern "C" int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, vo
   const int st = fa_validate_fwd_varlen(q, k, v, o, cu_seqlens, B, H, H_kv, max_seqlen, total, D);
   if (st != FA_OK) return st;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
-  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total};
+  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total, (int)B};
   return fa::fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream);
 }
 

@@ -307,6 +307,7 @@ struct Geom {
   int H;
   int group;
   int total;
+  int B;       // varlen: number of sequences
 };
 
 // One (b, h): element offsets of its Q/O and K/V rows, of its L row, and its
@@ -326,7 +327,11 @@ __device__ __forceinline__ HeadView head_view(const Geom& g, int bh) {
     v.kv = (size_t)(bh / g.group) * g.N * D;
     v.l = (size_t)bh * g.N;
   } else {
-    const int b = bh / g.H, h = bh - b * g.H;
+    // Head-major unit order (h, then b): the grid is cut into one contiguous
+    // range per XCD, and a range of whole heads holds every sequence's share
+    // of the work, where a range of whole sequences would give one XCD all of
+    // a long sequence.
+    const int h = bh / g.B, b = bh - h * g.B;
     const int s0 = min(max(g.cu[b], 0), g.total);
     const int s1 = min(max(g.cu[b + 1], s0), g.total);
     v.n = min(s1 - s0, g.N);
