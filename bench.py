@@ -38,9 +38,9 @@ def kernel_name(variant, D, causal=False, write_l=True, full=True):
     """Template instance of the forward kernel behind a variant code."""
     c, w, f = (str(x).lower() for x in (causal, write_l, full))
     if variant == 204:
-        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4>"
+        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4,false,2,1>"
     if variant == 308:
-        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},8,false,4>"
+        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},8,false,4,1>"
     if variant == 404:
         return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4,false,2,2>"
     if variant > 100:
