@@ -448,12 +448,36 @@ def main():
         oo = median_of(lambda: fa.forward_only(Q, K, V), 5, 10, 100, torch)
         wl = median_of(step, 5, 10, 100, torch)
         extra["N4096_O+L_vs_O-only_ms"] = [round(wl, 5), round(oo, 5)]
+        split_plan = fa.probe.probe_fwd_splitkv_plan
         for n in (1024, 2048, 8192):
             q, k, v = make_fwd(torch, dev, 1, 8, n, 64, seed=n)
-            ms = median_of(lambda: fa.forward(q, k, v), 5, 10, 200 if n <= 2048 else 50, torch)
+            it = 200 if n <= 2048 else 50
+            ms = median_of(lambda: fa.forward(q, k, v), 5, 10, it, torch)
             f = fwd_flops(1, 8, n, 64)
             extra[f"N{n}"] = {"ms": round(ms, 5), "TFLOPs": round(f / ms / 1e9, 1),
                               "pct_peak": round(100 * f / ms / 1e9 / PEAK_FP16_TFLOPS, 2)}
+            sp = split_plan(1, 8, n, 64, 0)
+            if sp > 1:   # the default path splits the keys here: the unsplit kernel beside it
+                ms1 = median_of(lambda: fa.probe.probe_fwd_splitkv(q, k, v, False, 1, True),
+                                5, 10, it, torch)
+                extra[f"N{n}"].update({"splits": sp, "unsplit_ms": round(ms1, 5)})
+        q, k, v = make_fwd(torch, dev, 1, 8, 4096, 64, seed=12)
+        ms = median_of(lambda: fa.forward(q, k, v, causal=True), 5, 10, 100, torch)
+        f = fwd_flops(1, 8, 4096, 64, causal=True)
+        extra["causal_B1H8N4096D64"] = {
+            "ms": round(ms, 5), "TFLOPs": round(f / ms / 1e9, 1),
+            "pct_peak": round(100 * f / ms / 1e9 / PEAK_FP16_TFLOPS, 2)}
+        # a long sequence over one head: 128 row blocks for 256 CUs, so the
+        # default path splits the keys in two
+        q, k, v = make_fwd(torch, dev, 1, 1, 16384, 64, seed=13)
+        ms = median_of(lambda: fa.forward(q, k, v), 5, 5, 20, torch)
+        ms1 = median_of(lambda: fa.probe.probe_fwd_splitkv(q, k, v, False, 1, True), 5, 5, 20,
+                        torch)
+        f = fwd_flops(1, 1, 16384, 64)
+        extra["B1H1N16384D64"] = {
+            "ms": round(ms, 5), "TFLOPs": round(f / ms / 1e9, 1),
+            "pct_peak": round(100 * f / ms / 1e9 / PEAK_FP16_TFLOPS, 2),
+            "splits": split_plan(1, 1, 16384, 64, 0), "unsplit_ms": round(ms1, 5)}
         q, k, v = make_fwd(torch, dev, 4, 16, 4096, 128, seed=3, amp=0.5)
         ms = median_of(lambda: fa.forward(q, k, v, causal=True), 5, 5, 20, torch)
         f = fwd_flops(4, 16, 4096, 128, causal=True)

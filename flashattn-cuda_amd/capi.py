@@ -49,6 +49,9 @@ SIGNATURES = {
     "fa_bwd_gqa_workspace_floats": (_i64, [_i64] * 5),
     "fa_bwd_gqa_f16": (C.c_int, [_vp] * 10 + [_i64] * 5 + [C.c_int, _vp]),
     "fa_bwd_bf16": (C.c_int, [_vp] * 10 + [_i64] * 5 + [C.c_int, _vp]),
+    "fa_fwd_splitkv_plan": (C.c_int, [_i64] * 4 + [C.c_int]),
+    "fa_fwd_splitkv_workspace_floats": (_i64, [_i64] * 5),
+    "fa_fwd_splitkv_f16": (C.c_int, [_vp] * 6 + [_i64] * 5 + [C.c_int, _i64, _vp]),
     "fa_bwd_varlen_f16": (C.c_int, [_vp] * 11 + [_i64] * 6 + [C.c_int, _vp]),
     "fa_validate_bwd_varlen": (C.c_int, [_vp] * 11 + [_i64] * 6),
     "fa_probe_fwd_variant": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp]),

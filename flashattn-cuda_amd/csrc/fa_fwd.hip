@@ -272,6 +272,29 @@ struct RowBlock {
       if (WRITE_L && hi == 0) Lh[qrow] = (m_run + log2_hw(l_tot)) * kLn2;
     }
   }
+
+  // Split-KV epilogue: this row's fp32 O normalised over the keys of one
+  // split and the natural-log LSE of those keys, at partial index `at` of a
+  // row-major [rows, splits] layout. A row that saw no key gets O = 0 and
+  // LSE = -inf (weight 0 in the combine).
+  __device__ __forceinline__ void finish_partial(float* part_o, float* part_lse, size_t at) const {
+    const float l_tot = sum_xor32(l_run);
+    if (FULL || qrow < N) {
+      const bool empty = l_tot == 0.f;
+      const float inv = empty ? 0.f : 1.f / l_tot;
+      float* orow = part_o + at * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v4 = f32x4{o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv,
+                                 o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+          *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * g + 4 * hi) = v4;
+        }
+      }
+      if (hi == 0) part_lse[at] = empty ? -INFINITY : (m_run + log2_hw(l_tot)) * kLn2;
+    }
+  }
 };
 
 // Per-lane DMA source offsets of 1 KiB block b of a tile: lane l writes bytes
@@ -769,11 +792,13 @@ fa_fwd_pipe_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // buffer range (zeros).
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false, int TG = 2,
-          int SUB = 1>
+          int SUB = 1, bool SPLITKV = false>
 __global__ void __launch_bounds__(256 * TG)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
-                 float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
+                 float* __restrict__ L, Geom geo, int num_qb, int total, float c,
+                 float* __restrict__ part_o = nullptr, float* __restrict__ part_lse = nullptr,
+                 int nsplit = 1) {
   // The unit of the ring and of a phase is a tile of SUB * 64 keys: SUB
   // consecutive 64-key key tiles ("sub-tiles", the unit of masking and of the
   // copies' bounds), NB 32-key blocks.
@@ -812,8 +837,11 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   auto tile_of = [&](int g, int j) { return TPS * j + g; };
 
   const int logical = xcd_remap(blockIdx.x, total);
-  const int bh = logical / num_qb;
-  int qb = logical - bh * num_qb;
+  // Split-KV: the splits of one q-block are adjacent (same XCD, same K/V).
+  const int split = SPLITKV ? logical % nsplit : 0;
+  const int unit = SPLITKV ? logical / nsplit : logical;
+  const int bh = unit / num_qb;
+  int qb = unit - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
 
   const HeadView hv = head_view<D>(geo, bh);
@@ -821,16 +849,32 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   if (qb * kBR >= N) return;   // varlen: past this sequence (whole workgroup)
   const size_t head = hv.q;
   const int head_bytes = N * D * 2;
-  const char* Kh = reinterpret_cast<const char*>(K + hv.kv);
-  const char* Vh = reinterpret_cast<const char*>(V + hv.kv);
   const int q0 = qb * kBR;
 
   RB rb;
   rb.init(Q + head, head_bytes, lane, q0 + 32 * rg, N, c);
 
   const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
-  const int n_sub = (kv_end + kBC - 1) / kBC;          // 64-key sub-tiles
-  const int n_tiles = (n_sub + SUB - 1) / SUB;
+  int n_sub = (kv_end + kBC - 1) / kBC;          // 64-key sub-tiles
+  int n_tiles = (n_sub + SUB - 1) / SUB;
+  // Split-KV: this workgroup's tiles are tb .. tb + n_tiles - 1 of the row
+  // block's; K/V pointers and bounds start at tile tb, masking uses absolute
+  // key positions (sub-tile offset tbs).
+  int tb = 0;
+  if constexpr (SPLITKV) {
+    const int per = (n_tiles + nsplit - 1) / nsplit;
+    tb = min(split * per, n_tiles);
+    n_tiles = min(per, n_tiles - tb);
+    n_sub = min(n_sub - tb * SUB, n_tiles * SUB);
+    if (n_tiles == 0) {   // nothing for this split: an empty partial for every row
+      if (grp == 0) rb.finish_partial(part_o, part_lse, (hv.l + rb.qrow) * nsplit + split);
+      return;
+    }
+  }
+  const int tbs = SPLITKV ? tb * SUB : 0;
+  const int kv_bytes = head_bytes - tbs * (kBC * D * 2);
+  const char* Kh = reinterpret_cast<const char*>(K + hv.kv) + (size_t)tbs * (kBC * D * 2);
+  const char* Vh = reinterpret_cast<const char*>(V + hv.kv) + (size_t)tbs * (kBC * D * 2);
   const int n_steps = (n_tiles + TPS - 1) / TPS;   // tiles per group
 
   const uint32_t lds0 = lds_addr(smem);
@@ -852,7 +896,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
       src = reinterpret_cast<const char*>(((uintptr_t)hi << 32) | lo);
     }
-    dma_block_or_zero<D, FULL>(src, head_bytes, st, st < n_sub, dst, off);
+    dma_block_or_zero<D, FULL>(src, kv_bytes, st, st < n_sub, dst, off);
   };
   // With four groups the per-lane offsets are recomputed where they are used
   // (from a lane id the compiler cannot hoist) instead of held in registers.
@@ -966,15 +1010,17 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // S phase: softmax of tile t (scores in s) into p, the exponentials of a
   // value pair consumed two pairs later.
   auto sphase = [&](int t) {
-    if (TG * SUB > 2 && t >= n_tiles) {
-      // a group's last tile can lie past the end: no keys, P = 0
+    if ((TG * SUB > 2 || SPLITKV) && t >= n_tiles) {
+      // A group's last tile can lie past the end: no keys, P = 0. (With two
+      // groups and no split, such a tile is past N and masked anyway; past a
+      // split's end its keys belong to the next split.)
 #pragma unroll
       for (int j = 0; j < 2 * NB; ++j) p[j] = f16x8{};
       wait_vmcnt<(RING / TPS - 2) * 2 * LOADS>();
       return;
     }
 #pragma unroll
-    for (int u = 0; u < SUB; ++u) rb.template mask<2>(SUB * t + u, 0, sub_s(u));
+    for (int u = 0; u < SUB; ++u) rb.template mask<2>(tbs + SUB * t + u, 0, sub_s(u));
     const float m_cur = rb.m_run;
     constexpr int PAIRS = 8 * NB;
     float ex[PAIRS][2];
@@ -1068,7 +1114,11 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   if (grp > 0) return;
 #pragma unroll
   for (int g = 1; g < TG; ++g) rb.merge_from(area + (g - 1) * REC);
-  rb.template finish<WRITE_L>(O + head, L + hv.l);
+  if constexpr (SPLITKV) {
+    rb.finish_partial(part_o, part_lse, (hv.l + rb.qrow) * nsplit + split);
+  } else {
+    rb.template finish<WRITE_L>(O + head, L + hv.l);
+  }
 }
 
 // Kernel variants: 10*k + s = split kernel with KSPLIT k and s LDS stages;
@@ -1235,6 +1285,91 @@ static int fwd_dense(const void* q, const void* k, const void* v, void* o, float
   return fwd_run(q, k, v, o, lse, geo, B, D, causal, variant, stream);
 }
 }  // namespace fa
+
+namespace fa {
+constexpr int kNumCUs = 256;   // MI355X
+
+// Split-KV forward: the ping-pong kernel over (row block, split) units writes
+// normalised fp32 partials and their LSEs; the decode's LSE combine, over the
+// B*H*N rows, merges them into O and L. For long sequences over few heads,
+// where the row blocks alone leave CUs idle.
+template <int D, bool CAUSAL, bool FULL>
+static hipError_t launch_splitkv(const f16* Q, const f16* K, const f16* V, f16* O, float* L,
+                                 const Geom& geo, int num_qb, int units, float c, float* part_o,
+                                 float* part_lse, int nsplit, int64_t rows, hipStream_t s) {
+  hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, true, FULL, 4, false, 2, 1, true>),
+                     dim3(units * nsplit), dim3(512), 0, s, Q, K, V, O, L, geo, num_qb,
+                     units * nsplit, c, part_o, part_lse, nsplit);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int st = fa_lse_combine_f32(part_o, part_lse, rows, 1, D, nsplit, O, L, s);
+  return st == FA_OK ? hipSuccess : hipErrorInvalidValue;
+}
+}  // namespace fa
+
+extern "C" int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal) {
+  if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128)) return 1;
+  // Measured: a split pays where the row blocks leave CUs idle and each split
+  // still has >= 32 key tiles (B1 H1 N16384: 122 -> 88 us with 2 splits);
+  // with fewer tiles per workgroup its fixed costs and the combine pass
+  // dominate (B1 H8 N1024: 11.5 -> 12.8 us + 7 us), and causal triangles did
+  // not even out (B1 H8 N4096 causal: 36.5 -> 42.6 us).
+  if (causal) return 1;
+  const int64_t units = B * H * ((N + fa::kBR - 1) / fa::kBR);
+  const int64_t tiles = (N + fa::kBC - 1) / fa::kBC;   // key tiles of a row block
+  if (units >= fa::kNumCUs) return 1;
+  int64_t sp = (fa::kNumCUs + units - 1) / units;
+  sp = sp < tiles / 32 ? sp : tiles / 32;
+  sp = sp < 8 ? sp : 8;
+  return sp < 2 ? 1 : (int)sp;
+}
+
+extern "C" int64_t fa_fwd_splitkv_workspace_floats(int64_t B, int64_t H, int64_t N, int64_t D,
+                                                   int64_t num_splits) {
+  if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128) || num_splits < 1) return 0;
+  return B * H * N * num_splits * (D + 1);   // partial O, then the partial LSEs
+}
+
+extern "C" int fa_fwd_splitkv_f16(const void* q, const void* k, const void* v, void* o,
+                                  float* lse, float* workspace, int64_t B, int64_t H,
+                                  int64_t H_kv, int64_t N, int64_t D, int causal,
+                                  int64_t num_splits, void* stream) {
+  using namespace fa;
+  int st = fa_validate_fwd_gqa(q, k, v, o, B, H, H_kv, N, D);
+  if (st != FA_OK) return st;
+  if (workspace == nullptr) return FA_ERR_NULL_POINTER;
+  if (num_splits < 1 || num_splits > 16) return FA_ERR_NUM_SPLITS;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
+  if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
+  const int64_t num_qb = (N + kBR - 1) / kBR;
+  if (B * H * num_qb > (int64_t(1) << 31) / num_splits) return FA_ERR_TOO_LARGE;
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  const int units = (int)(B * H * num_qb);
+  const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  const bool full = (N % kBR) == 0;
+  const int64_t rows = B * H * N;
+  float* part_o = workspace;
+  float* part_lse = workspace + rows * num_splits * D;
+  const f16* Q = (const f16*)q;
+  const f16* K = (const f16*)k;
+  const f16* V = (const f16*)v;
+  f16* Op = (f16*)o;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int ns = (int)num_splits;
+  const int nq = (int)num_qb;
+  hipError_t e;
+#define FA_SPLITKV(DD, CC, FF) \
+  launch_splitkv<DD, CC, FF>(Q, K, V, Op, lse, geo, nq, units, c, part_o, part_lse, ns, rows, s)
+  if (D == 64) {
+    e = causal ? (full ? FA_SPLITKV(64, true, true) : FA_SPLITKV(64, true, false))
+               : (full ? FA_SPLITKV(64, false, true) : FA_SPLITKV(64, false, false));
+  } else {
+    e = causal ? (full ? FA_SPLITKV(128, true, true) : FA_SPLITKV(128, true, false))
+               : (full ? FA_SPLITKV(128, false, true) : FA_SPLITKV(128, false, false));
+  }
+#undef FA_SPLITKV
+  return e == hipSuccess ? FA_OK : -(int)e;
+}
 
 extern "C" int fa_fwd_f16(const void* q, const void* k, const void* v, void* o,
                           float* lse, int64_t B, int64_t H, int64_t N, int64_t D,

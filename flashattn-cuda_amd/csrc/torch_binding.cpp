@@ -31,9 +31,12 @@ void check_status(int st, const char* what) {
   TORCH_CHECK(st == FA_OK, what, " failed: ", fa_status_str(st), " (status ", st, ")");
 }
 
+// variant 0: the default kernel, split over the keys where
+// fa_fwd_splitkv_plan asks for it (few row blocks, or causal at small B*H);
+// variant > 0: one explicit kernel variant; splits > 0: that split count.
 std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Tensor K,
                                                      torch::Tensor V, bool want_L, bool causal,
-                                                     int variant = 0) {
+                                                     int variant = 0, int64_t splits = 0) {
   TORCH_CHECK(Q.is_cuda() && K.is_cuda() && V.is_cuda(), "Q/K/V must be CUDA tensors");
   TORCH_CHECK(Q.dim() == 4, "Q must be 4D [B, H, N, D]");
   const int64_t B = Q.size(0), H = Q.size(1), N = Q.size(2), D = Q.size(3);
@@ -63,12 +66,22 @@ std::pair<torch::Tensor, torch::Tensor> forward_impl(torch::Tensor Q, torch::Ten
     L_ptr = L.data_ptr<float>();
   }
   TORCH_CHECK(variant == 0 || Hkv == H, "explicit kernel variants take H_kv == H");
-  const int st =
-      variant == 0
-          ? fa_fwd_gqa_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H,
-                           Hkv, N, D, causal ? 1 : 0, current_stream(Qh))
-          : fa_probe_fwd_variant(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr,
-                                 B, H, N, D, causal ? 1 : 0, variant, current_stream(Qh));
+  const int64_t nsplit =
+      variant != 0 ? 1 : (splits > 0 ? splits : fa_fwd_splitkv_plan(B, H, N, D, causal ? 1 : 0));
+  int st;
+  if (nsplit > 1) {
+    auto ws = torch::empty({fa_fwd_splitkv_workspace_floats(B, H, N, D, nsplit)},
+                           Qh.options().dtype(torch::kFloat));
+    st = fa_fwd_splitkv_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr,
+                            ws.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, nsplit,
+                            current_stream(Qh));
+  } else if (variant == 0) {
+    st = fa_fwd_gqa_f16(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr, B, H,
+                        Hkv, N, D, causal ? 1 : 0, current_stream(Qh));
+  } else {
+    st = fa_probe_fwd_variant(Qh.data_ptr(), Kh.data_ptr(), Vh.data_ptr(), O.data_ptr(), L_ptr,
+                              B, H, N, D, causal ? 1 : 0, variant, current_stream(Qh));
+  }
   check_status(st, "fa_fwd_f16");
   return {O.reshape({B, H, N, D}), want_L ? L.reshape({B, H, N}) : torch::Tensor()};
 }
@@ -269,6 +282,17 @@ std::vector<torch::Tensor> probe_fwd_variant(torch::Tensor Q, torch::Tensor K, t
                                              bool causal, int64_t variant, bool want_L) {
   TORCH_CHECK(variant > 0, "variant must be > 0");
   auto r = forward_impl(Q, K, V, want_L, causal, (int)variant);
+  if (want_L) return {r.first, r.second};
+  return {r.first};
+}
+
+// Test support: the forward split over the keys into an explicit number of
+// ranges (1 = the unsplit default kernel).
+std::vector<torch::Tensor> probe_fwd_splitkv(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
+                                             bool causal, int64_t splits, bool want_L) {
+  TORCH_CHECK(splits >= 1 && splits <= 16, "splits must be in [1, 16]");
+  auto r = splits == 1 ? forward_impl(Q, K, V, want_L, causal, /*variant=*/204)
+                       : forward_impl(Q, K, V, want_L, causal, 0, splits);
   if (want_L) return {r.first, r.second};
   return {r.first};
 }
@@ -538,6 +562,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("probe_fwd_variant", &probe_fwd_variant, py::arg("Q"), py::arg("K"), py::arg("V"),
         py::arg("causal") = false, py::arg("variant") = 12, py::arg("want_L") = true);
   m.def("probe_fwd_variants", &probe_fwd_variants);
+  m.def("probe_fwd_splitkv", &probe_fwd_splitkv,
+            "forward split over the keys into `splits` ranges ([O, L] or [O])", py::arg("Q"),
+            py::arg("K"), py::arg("V"), py::arg("causal"), py::arg("splits"), py::arg("want_L"));
+  m.def("probe_fwd_splitkv_plan", &fa_fwd_splitkv_plan, "split count the forward uses",
+            py::arg("B"), py::arg("H"), py::arg("N"), py::arg("D"), py::arg("causal"));
   m.def("probe_default_variant", [](int64_t D) { return fa_probe_default_variant(D); });
   m.def("abi_version", &fa_abi_version);
 }

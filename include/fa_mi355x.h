@@ -208,6 +208,23 @@ int fa_validate_bwd_varlen(const void* q, const void* k, const void* v, const vo
                            int64_t total, int64_t D);
 
 /*
+ * Split-KV forward (no reference counterpart): fa_fwd_gqa_f16's result with
+ * each 128-row block's keys cut into num_splits ranges run as separate
+ * workgroups, then merged by the LSE combine (fills the GPU when B*H*N/128
+ * row blocks are fewer than the CUs and the sequences are long). O within the
+ * forward's tolerance of the unsplit kernel; lse nullable (O only). The
+ * workspace (fa_fwd_splitkv_workspace_floats floats, 16-byte aligned) holds
+ * the fp32 partials. fa_fwd_splitkv_plan returns the split count the torch
+ * binding uses (1: no split) for a shape.
+ */
+int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal);
+int64_t fa_fwd_splitkv_workspace_floats(int64_t B, int64_t H, int64_t N, int64_t D,
+                                        int64_t num_splits);
+int fa_fwd_splitkv_f16(const void* q, const void* k, const void* v, void* o, float* lse,
+                       float* workspace, int64_t B, int64_t H, int64_t H_kv, int64_t N,
+                       int64_t D, int causal, int64_t num_splits, void* stream);
+
+/*
  * Host-only argument check of the decode entry points. No reference
  * counterpart (the reference has no decode path).
  */

@@ -264,3 +264,54 @@ def test_every_kernel_variant(fa, dev, D):
             torch.cuda.synchronize()
             assert torch.equal(O, O2), f"variant {v}: O-only differs"
             _check(O, L, Or, Lr, 1.0, tag=f"variant {v} B{B} H{H} N{N} D{D} causal={causal}")
+
+
+# Split-KV forward: each row block's keys cut into `splits` ranges run as
+# separate workgroups, then merged by the LSE combine (the decode's a13 math).
+# Same tolerance as the unsplit kernel; more splits than key tiles leaves
+# empty ranges (LSE -inf, weight 0).
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,H,N,causal", [(1, 2, 300, True), (1, 2, 1024, False),
+                                          (2, 3, 1000, True), (1, 2, 4096, True),
+                                          (1, 1, 100, False)])
+@pytest.mark.parametrize("splits", [2, 3, 8])
+def test_splitkv_forward(fa, dev, D, B, H, N, causal, splits):
+    Q, K, V = make_fwd_inputs(B, H, N, D, seed=N + D + splits, amp=1.0)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O, L = fa.probe.probe_fwd_splitkv(tq, tk, tv, causal, splits, True)
+    (O2,) = fa.probe.probe_fwd_splitkv(tq, tk, tv, causal, splits, False)
+    torch.cuda.synchronize()
+    assert torch.equal(O, O2), "O-only differs from O+L"
+    Or, Lr = naive_attention(half_cast(Q), half_cast(K), half_cast(V), causal=causal)
+    _check(O, L, Or, Lr, 1.0, tag=f"split {splits} B{B} H{H} N{N} D{D} causal={causal}")
+
+
+def test_splitkv_plan_and_default_path(fa, dev):
+    """The default forward splits the keys only for long sequences over few
+    heads, and stays close to the unsplit kernel there (same inputs,
+    different summation order)."""
+    p = fa.probe.probe_fwd_splitkv_plan
+    assert p(1, 8, 4096, 64, 0) == 1          # the headline keeps the unsplit kernel
+    assert p(1, 8, 4096, 64, 1) == 1          # causal never splits
+    assert p(1, 8, 1024, 64, 0) == 1          # too few key tiles per split
+    assert p(1, 1, 16384, 64, 0) == 2
+    assert p(1, 1, 8192, 128, 0) == 4
+    Q, K, V = make_fwd_inputs(1, 1, 8192, 128, seed=77, amp=1.0)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    Od, Ld = fa.forward(tq, tk, tv)
+    Ou, Lu = fa.probe.probe_fwd_splitkv(tq, tk, tv, False, 1, True)
+    assert (Od.float() - Ou.float()).abs().max().item() <= 2e-3
+    assert ((Ld - Lu).abs() / Lu.abs().clamp(min=1)).max().item() <= 1e-5
+
+
+def test_splitkv_gqa(fa, dev):
+    B, H, Hkv, N, D = 2, 8, 2, 700, 64
+    rng = np.random.default_rng(5)
+    Q = rng.standard_normal((B, H, N, D)).astype(np.float32)
+    K = rng.standard_normal((B, Hkv, N, D)).astype(np.float32)
+    V = rng.standard_normal((B, Hkv, N, D)).astype(np.float32)
+    tq, tk, tv = (torch.from_numpy(x).to(dev) for x in (Q, K, V))
+    O, L = fa.probe.probe_fwd_splitkv(tq, tk, tv, True, 3, True)
+    Or, Lr = naive_attention(half_cast(Q), np.repeat(half_cast(K), H // Hkv, axis=1),
+                             np.repeat(half_cast(V), H // Hkv, axis=1), causal=True)
+    _check(O, L, Or, Lr, 1.0, tag="split GQA")
