@@ -75,16 +75,32 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
   for (int i = 0; i < DPL; ++i) o[i] = 0.f;
 
   const int32_t* pt = page_table + (size_t)b * max_pages;
-  for (int p = p0 + wave; p < p1; p += kDecWaves) {
+  const int kvh = h / (H / Hkv);
+  // The wave's next page is loaded into (kn, vn) before the current one is
+  // used, so one page per wave is always in flight behind the arithmetic.
+  f16x8 kn[NV], vn[NV];
+  bool ok_n = false;
+  auto load_page = [&](int p) {
     const int pid = pt[p];
-    if (pid < 0 || pid >= num_pages) { bad = true; continue; }
-    const size_t base = ((size_t)pid * Hkv + h / (H / Hkv)) * (kPage * D) + (size_t)tok * D +
-                        dq * DPL;
+    ok_n = pid >= 0 && pid < num_pages;
+    if (!ok_n) return;
+    const size_t base = ((size_t)pid * Hkv + kvh) * (kPage * D) + (size_t)tok * D + dq * DPL;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) kn[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) vn[i] = *reinterpret_cast<const f16x8*>(vpool + base + 8 * i);
+  };
+  if (p0 + wave < p1) load_page(p0 + wave);
+  for (int p = p0 + wave; p < p1; p += kDecWaves) {
     f16x8 kv[NV], vv[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const f16x8*>(vpool + base + 8 * i);
+    for (int i = 0; i < NV; ++i) {
+      kv[i] = kn[i];
+      vv[i] = vn[i];
+    }
+    const bool ok = ok_n;
+    if (p + kDecWaves < p1) load_page(p + kDecWaves);
+    if (!ok) { bad = true; continue; }
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
