@@ -94,12 +94,30 @@ def make_fwd(torch, dev, B, H, N, D, seed, amp=1.0):
     return [(torch.randn(B, H, N, D, device=dev, generator=g) * amp).half() for _ in range(3)]
 
 
+def decode_meta(B=32, ctx_lo=512, ctx_hi=32768, page_size=16, seed=5):
+    """Config 5's synthetic paging: context lengths ~ U[ctx_lo, ctx_hi] and a
+    page table that is one random permutation of the pool's page ids (every
+    page used once). Returns (ctx_lens int32 [B], page_table int32 [B,
+    max_pages], num_pages)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(ctx_lo, ctx_hi + 1, size=B).astype(np.int32)
+    pages = (ctx + page_size - 1) // page_size
+    num_pages = int(pages.sum())
+    perm = rng.permutation(num_pages).astype(np.int32)
+    table = np.zeros((B, int(pages.max())), dtype=np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    return ctx, table, num_pages
+
+
 def bench_decode(fa, torch, dev, reps=5, iters=20):
     import numpy as np
-    from oracle import make_decode_meta  # seeded metadata generator only (no oracle math)
 
     B, H, D, S = 32, 32, 128, 16
-    ctx, table, P = make_decode_meta(B=B, seed=5)
+    ctx, table, P = decode_meta(B=B, seed=5)
     g = torch.Generator(device=dev).manual_seed(5)
     kp = torch.randn(P, H, 16, D, device=dev, dtype=torch.float16, generator=g)
     vp = torch.randn(P, H, 16, D, device=dev, dtype=torch.float16, generator=g)
@@ -367,8 +385,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
-              f"(the forward and decode shard with no communication; see DESIGN.md)",
-              file=sys.stderr)
+              f"(the forward and the decode shard over heads and sequences with no "
+              f"communication, so one GPU's share is the per-GPU workload)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -493,3 +493,18 @@ def test_planted_bf16_truncation_is_caught():
     x = np.random.default_rng(13).standard_normal(1000).astype(np.float32)
     trunc = (x.view(np.uint32) >> 16 << 16).view(np.float32)   # round toward zero
     assert not np.array_equal(trunc, torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+def test_bench_decode_metadata_matches_the_oracle_generator():
+    """bench.py builds config 5's paging itself (the bench may not call the
+    oracle outside its CPU-baseline leg); it must be the tests' metadata."""
+    import importlib.util
+    import pathlib
+    path = pathlib.Path(__file__).resolve().parents[1] / "bench.py"
+    spec = importlib.util.spec_from_file_location("fa_bench", path)
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for seed in (5, 6):
+        a = bench.decode_meta(B=32, seed=seed)
+        b = orc.make_decode_meta(B=32, seed=seed)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]) and a[2] == b[2]
