@@ -25,6 +25,8 @@
 // swizzle, so both reads stay bank-conflict free.
 #include <hip/hip_runtime.h>
 
+#include <stdlib.h>
+
 #include <math.h>
 #include <stdint.h>
 
@@ -198,12 +200,12 @@ __device__ __forceinline__ void group_reduce(char* smem, int grp, int slot, int 
 // transposed swizzle) and 64 floats each of NL and D_i.
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, int G, bool BF16>
-__global__ void __launch_bounds__(256 * G)
-fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
-                   const f16* __restrict__ V, const f16* __restrict__ dO,
-                   const float* __restrict__ NL, const float* __restrict__ Di,
-                   float* __restrict__ dK, float* __restrict__ dV, Geom geo, int num_kb,
-                   int total, float c, float scale) {
+__device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* __restrict__ K,
+                                          const f16* __restrict__ V, const f16* __restrict__ dO,
+                                          const float* __restrict__ NL,
+                                          const float* __restrict__ Di, float* __restrict__ dK,
+                                          float* __restrict__ dV, const Geom& geo, int num_kb,
+                                          int total, float c, float scale, int block) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
@@ -220,7 +222,7 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int kw = wave & 3;
   const int grp = wave >> 2;
   const int hi = lane >> 5;
-  const int logical = xcd_remap(blockIdx.x, total);
+  const int logical = xcd_remap(block, total);
   const int bh = logical / num_kb;
   const int kb = logical - bh * num_kb;
   const int k0 = kb * kBlk;
@@ -365,12 +367,12 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // transposed swizzle) and V once (row swizzle).
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, int G, bool BF16>
-__global__ void __launch_bounds__(256 * G)
-fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
-                 const f16* __restrict__ V, const f16* __restrict__ dO,
-                 const float* __restrict__ NL, const float* __restrict__ Di,
-                 float* __restrict__ dQ, Geom geo, int num_qb, int total, float c,
-                 float scale) {
+__device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __restrict__ K,
+                                        const f16* __restrict__ V, const f16* __restrict__ dO,
+                                        const float* __restrict__ NL,
+                                        const float* __restrict__ Di, float* __restrict__ dQ,
+                                        const Geom& geo, int num_qb, int total, float c,
+                                        float scale, int block) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
@@ -387,7 +389,7 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int qw = wave & 3;
   const int grp = wave >> 2;
   const int hi = lane >> 5;
-  const int logical = xcd_remap(blockIdx.x, total);
+  const int logical = xcd_remap(block, total);
   const int bh = logical / num_qb;
   int qb = logical - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows first
@@ -505,6 +507,49 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // GQA: dK, dV of KV head hk = sum over its `group` query heads of the
 // per-query-head partials (fp32 [B*H, N*D] -> [B*Hkv, N*D]), four floats per
 // thread.
+template <int D, bool CAUSAL, int G, bool BF16>
+__global__ void __launch_bounds__(256 * G)
+fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                   const f16* __restrict__ V, const f16* __restrict__ dO,
+                   const float* __restrict__ NL, const float* __restrict__ Di,
+                   float* __restrict__ dK, float* __restrict__ dV, Geom geo, int num_kb,
+                   int total, float c, float scale) {
+  dkdv_body<D, CAUSAL, G, BF16>(Q, K, V, dO, NL, Di, dK, dV, geo, num_kb, total, c, scale,
+                                (int)blockIdx.x);
+}
+
+template <int D, bool CAUSAL, int G, bool BF16>
+__global__ void __launch_bounds__(256 * G)
+fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                 const f16* __restrict__ V, const f16* __restrict__ dO,
+                 const float* __restrict__ NL, const float* __restrict__ Di,
+                 float* __restrict__ dQ, Geom geo, int num_qb, int total, float c,
+                 float scale) {
+  dq_body<D, CAUSAL, G, BF16>(Q, K, V, dO, NL, Di, dQ, geo, num_qb, total, c, scale,
+                              (int)blockIdx.x);
+}
+
+// dK/dV and dQ in one launch (D = 64, where both take 8 waves): blocks
+// [0, total) are the dK/dV kernel's, [total, 2 total) the dQ kernel's. Each
+// half is dispatched longest unit first, so a CU that finished a short dK/dV
+// unit (late keys of a causal head) picks up a long dQ unit: the causal
+// triangle's two halves even out across the CUs instead of each kernel
+// waiting for its own longest unit.
+template <int D, bool CAUSAL, bool BF16>
+__global__ void __launch_bounds__(512)
+fa_bwd_fused_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                    const f16* __restrict__ V, const f16* __restrict__ dO,
+                    const float* __restrict__ NL, const float* __restrict__ Di,
+                    float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ dQ,
+                    Geom geo, int nb, int total, float c, float scale) {
+  const int blk = (int)blockIdx.x;
+  if (blk < total) {
+    dkdv_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, Di, dK, dV, geo, nb, total, c, scale, blk);
+  } else {
+    dq_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, Di, dQ, geo, nb, total, c, scale, blk - total);
+  }
+}
+
 __global__ void __launch_bounds__(256)
 fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out, int64_t head_elems,
                         int64_t kv_heads, int group) {
@@ -556,10 +601,26 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const int nb = (geo.N + kBlk - 1) / kBlk;
   const int total = (int)(units * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
-  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
-                     V, G, nl, di, dk_q, dv_q, geo, nb, total, c, scale);
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ, BF16>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
-                     G, nl, di, dq, geo, nb, total, c, scale);
+  // FA_MI355X_BWD_FUSED=0 (read once) launches the two kernels separately,
+  // for measurement.
+  static const bool fused = [] {
+    const char* e = getenv("FA_MI355X_BWD_FUSED");
+    return !(e && e[0] == '0');
+  }();
+  bool launched = false;
+  if constexpr (GK == 2 && GQ == 2) {   // D = 64: both kernels take 8 waves
+    if (fused) {
+      hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
+                         s, Q, K, V, G, nl, di, dk_q, dv_q, dq, geo, nb, total, c, scale);
+      launched = true;
+    }
+  }
+  if (!launched) {
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
+                       V, G, nl, di, dk_q, dv_q, geo, nb, total, c, scale);
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ, BF16>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
+                       G, nl, di, dq, geo, nb, total, c, scale);
+  }
   if (group > 1) {
     // out_heads KV heads of head_rows rows, each the sum of `group`
     // consecutive query heads' partials
