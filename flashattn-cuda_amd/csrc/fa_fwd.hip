@@ -256,21 +256,84 @@ struct RowBlock {
   template <bool WRITE_L>
   __device__ __forceinline__ void finish(f16* Oh, float* Lh) const {
     const float l_tot = sum_xor32(l_run);
+    const float inv = 1.f / l_tot;
+    // Lanes l and l^32 hold the two 8-byte halves of each 16-byte chunk
+    // (columns 32 db + 8 g .. +7) of the row. One permlane32 swap per
+    // register of a chunk pair (g, g+1) gives lane l (hi = 0) all of chunk g
+    // and lane l^32 all of chunk g+1, so every lane stores whole 16-byte
+    // chunks: half the store instructions, 32 bytes of a row per lane pair.
+    uint4 st[DB][2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        uint32_t w[2][2];   // [chunk g0 or g0+1][register]
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int g = 2 * gp + j;
+          const f16x2 a = cvt2x<BF16>(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv);
+          const f16x2 b = cvt2x<BF16>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+          w[j][0] = __builtin_bit_cast(uint32_t, a);
+          w[j][1] = __builtin_bit_cast(uint32_t, b);
+        }
+        const auto r0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
+        const auto r1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
+        st[db][gp] = uint4{r0[0], r1[0], r0[1], r1[1]};
+      }
+    }
     if (FULL || qrow < N) {
-      const float inv = 1.f / l_tot;
       f16* orow = Oh + (size_t)qrow * D;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          f16x2 a = cvt2x<BF16>(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv);
-          f16x2 b = cvt2x<BF16>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-          f16x4 v4 = f16x4{a[0], a[1], b[0], b[1]};
-          *reinterpret_cast<f16x4*>(orow + 32 * db + 8 * g + 4 * hi) = v4;
-        }
+        for (int gp = 0; gp < 2; ++gp)
+          *reinterpret_cast<uint4*>(orow + 32 * db + 8 * (2 * gp + hi)) = st[db][gp];
       }
       if (WRITE_L && hi == 0) Lh[qrow] = (m_run + log2_hw(l_tot)) * kLn2;
     }
+  }
+
+  // finish<WRITE_L> with O staged through this wave's `stage` LDS area (at
+  // least 32 rows of STAGE_STRIDE bytes, written and read only by this wave):
+  // each lane writes its 16-byte chunks, then 8 lanes store one 128-byte
+  // (D = 64) or two (D = 128) rows, so a store instruction covers whole rows
+  // instead of 32-byte pieces of 32 rows.
+  static constexpr int STAGE_STRIDE = 2 * D + 16;   // padded: spreads the LDS banks
+  template <bool WRITE_L>
+  __device__ __forceinline__ void finish_staged(f16* Oh, float* Lh, char* stage) const {
+    const float l_tot = sum_xor32(l_run);
+    const float inv = 1.f / l_tot;
+    constexpr int CPR = D / 8;                       // 16-byte chunks per row
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        uint32_t w[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int g = 2 * gp + j;
+          const f16x2 a = cvt2x<BF16>(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv);
+          const f16x2 b = cvt2x<BF16>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+          w[j][0] = __builtin_bit_cast(uint32_t, a);
+          w[j][1] = __builtin_bit_cast(uint32_t, b);
+        }
+        const auto r0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
+        const auto r1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
+        const int chunk = 4 * db + 2 * gp + hi;      // 16-byte chunk of the row
+        *reinterpret_cast<uint4*>(stage + (lane & 31) * STAGE_STRIDE + chunk * 16) =
+            uint4{r0[0], r1[0], r0[1], r1[1]};
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS writes landed
+#pragma unroll
+    for (int k = 0; k < 32 * CPR / 64; ++k) {
+      const int idx = 64 * k + lane;
+      const int r = idx / CPR, ch = idx % CPR;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * STAGE_STRIDE + ch * 16);
+      if (FULL || row_w + r < N)
+        *reinterpret_cast<uint4*>(Oh + (size_t)(row_w + r) * D + ch * 8) = v;
+    }
+    if (WRITE_L && hi == 0 && (FULL || qrow < N)) Lh[qrow] = (m_run + log2_hw(l_tot)) * kLn2;
   }
 
   // Split-KV epilogue: this row's fp32 O normalised over the keys of one
@@ -1117,7 +1180,9 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   if constexpr (SPLITKV) {
     rb.finish_partial(part_o, part_lse, (hv.l + rb.qrow) * nsplit + split);
   } else {
-    rb.template finish<WRITE_L>(O + head, L + hv.l);
+    // this wave's merge record is read; its area stages the O tile
+    static_assert(32 * RB::STAGE_STRIDE <= REC * 4, "O staging exceeds the merge record");
+    rb.template finish_staged<WRITE_L>(O + head, L + hv.l, reinterpret_cast<char*>(area));
   }
 }
 
