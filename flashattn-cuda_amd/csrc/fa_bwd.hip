@@ -199,23 +199,30 @@ __device__ __forceinline__ void group_reduce(char* smem, int grp, int slot, int 
 // stream through 2 LDS stages; each stage holds Q and dO twice (row swizzle,
 // transposed swizzle) and 64 floats each of NL and D_i.
 // ---------------------------------------------------------------------------
+// LDS bytes of the dK/dV body: two stages, or the group reduction's
+// 2 (dK, dV) x DB x 16 floats per lane of 4 waves, whichever is larger.
+template <int D, int G>
+constexpr int dkdv_smem() {
+  constexpr int STAGE = 4 * (kBQ * D * 2) + 2048;   // Qk | Qv | dOk | dOv | NL | D_i
+  constexpr int RED = (G - 1) * 4 * 2 * (D / 32) * 16 * 64 * 4;
+  return 2 * STAGE > RED ? 2 * STAGE : RED;
+}
+
 template <int D, bool CAUSAL, int G, bool BF16>
 __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* __restrict__ K,
                                           const f16* __restrict__ V, const f16* __restrict__ dO,
                                           const float* __restrict__ NL,
                                           const float* __restrict__ Di, float* __restrict__ dK,
                                           float* __restrict__ dV, const Geom& geo, int num_kb,
-                                          int total, float c, float scale, int block) {
+                                          int total, float c, float scale, int block,
+                                          char* smem /* dkdv_smem<D, G>() bytes, 1 KiB aligned */) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
   constexpr int STAGE = 4 * TILE + 2048;       // Qk | Qv | dOk | dOv | NL | D_i
   constexpr int WAVES = 4 * G;
   constexpr int LOADS = 4 * BLOCKS / WAVES;    // tile blocks per wave per stage
-  constexpr int SMEM = 2 * STAGE > (G - 1) * 4 * 2 * DB * 16 * 64 * 4
-                           ? 2 * STAGE : (G - 1) * 4 * 2 * DB * 16 * 64 * 4;
   static_assert(4 * BLOCKS % WAVES == 0, "copy blocks split evenly over the waves");
-  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -366,13 +373,23 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
 // 64 rows stream through 2 LDS stages, each holding K twice (row swizzle,
 // transposed swizzle) and V once (row swizzle).
 // ---------------------------------------------------------------------------
+// LDS bytes of the dQ body: two stages, or the group reduction's DB x 16
+// floats per lane of 4 waves, whichever is larger.
+template <int D, int G>
+constexpr int dq_smem() {
+  constexpr int STAGE = 3 * (kBQ * D * 2);    // Kk | Kv | Vk
+  constexpr int RED = (G - 1) * 4 * (D / 32) * 16 * 64 * 4;
+  return 2 * STAGE > RED ? 2 * STAGE : RED;
+}
+
 template <int D, bool CAUSAL, int G, bool BF16>
 __device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __restrict__ K,
                                         const f16* __restrict__ V, const f16* __restrict__ dO,
                                         const float* __restrict__ NL,
                                         const float* __restrict__ Di, float* __restrict__ dQ,
                                         const Geom& geo, int num_qb, int total, float c,
-                                        float scale, int block) {
+                                        float scale, int block,
+                                        char* smem /* dq_smem<D, G>() bytes, 1 KiB aligned */) {
   constexpr int TILE = kBQ * D * 2;
   constexpr int BLOCKS = TILE / 1024;
   constexpr int KSTEPS = D / 16, DB = D / 32;
@@ -380,9 +397,6 @@ __device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __
   constexpr int NBLK = 3 * BLOCKS;
   constexpr int WAVES = 4 * G;
   constexpr int LOADS = (NBLK + WAVES - 1) / WAVES;   // tile blocks per wave per stage
-  constexpr int SMEM = 2 * STAGE > (G - 1) * 4 * DB * 16 * 64 * 4
-                           ? 2 * STAGE : (G - 1) * 4 * DB * 16 * 64 * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -514,8 +528,9 @@ fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const float* __restrict__ NL, const float* __restrict__ Di,
                    float* __restrict__ dK, float* __restrict__ dV, Geom geo, int num_kb,
                    int total, float c, float scale) {
+  __shared__ __attribute__((aligned(1024))) char smem[dkdv_smem<D, G>()];
   dkdv_body<D, CAUSAL, G, BF16>(Q, K, V, dO, NL, Di, dK, dV, geo, num_kb, total, c, scale,
-                                (int)blockIdx.x);
+                                (int)blockIdx.x, smem);
 }
 
 template <int D, bool CAUSAL, int G, bool BF16>
@@ -525,12 +540,14 @@ fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const float* __restrict__ NL, const float* __restrict__ Di,
                  float* __restrict__ dQ, Geom geo, int num_qb, int total, float c,
                  float scale) {
+  __shared__ __attribute__((aligned(1024))) char smem[dq_smem<D, G>()];
   dq_body<D, CAUSAL, G, BF16>(Q, K, V, dO, NL, Di, dQ, geo, num_qb, total, c, scale,
-                              (int)blockIdx.x);
+                              (int)blockIdx.x, smem);
 }
 
-// dK/dV and dQ in one launch (D = 64, where both take 8 waves): blocks
-// [0, total) are the dK/dV kernel's, [total, 2 total) the dQ kernel's. Each
+// dK/dV and dQ in one launch (both bodies take 8 waves and share one LDS
+// buffer): blocks [0, total) are the dK/dV kernel's, [total, 2 total) the dQ
+// kernel's. Each
 // half is dispatched longest unit first, so a CU that finished a short dK/dV
 // unit (late keys of a causal head) picks up a long dQ unit: the causal
 // triangle's two halves even out across the CUs instead of each kernel
@@ -542,11 +559,16 @@ fa_bwd_fused_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                     const float* __restrict__ NL, const float* __restrict__ Di,
                     float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ dQ,
                     Geom geo, int nb, int total, float c, float scale) {
+  // one LDS buffer serves whichever body this workgroup runs
+  constexpr int SK = dkdv_smem<D, 2>(), SQ = dq_smem<D, 2>();
+  __shared__ __attribute__((aligned(1024))) char smem[SK > SQ ? SK : SQ];
   const int blk = (int)blockIdx.x;
   if (blk < total) {
-    dkdv_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, Di, dK, dV, geo, nb, total, c, scale, blk);
+    dkdv_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, Di, dK, dV, geo, nb, total, c, scale, blk,
+                                  smem);
   } else {
-    dq_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, Di, dQ, geo, nb, total, c, scale, blk - total);
+    dq_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, Di, dQ, geo, nb, total, c, scale, blk - total,
+                                smem);
   }
 }
 
@@ -565,11 +587,14 @@ fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
   reinterpret_cast<f32x4*>(out)[i4] = acc;
 }
 
-// Wave groups per workgroup: two where the registers allow two waves per SIMD
-// (the second group takes the other half of every tile, so the grid stays
-// one workgroup per 128 rows and the SIMDs get a second wave to overlap).
+// Wave groups per workgroup: two (the second group takes the other half of
+// every tile, so the grid stays one workgroup per 128 rows and the SIMDs get
+// a second wave to overlap). At D = 128 the dK/dV body then needs more than
+// the 256 VGPRs two waves per SIMD allow and spills 10 of them (36 bytes of
+// scratch per lane); measured on B4 H16 N4096 causal it still beats one group
+// (281 VGPRs, one wave per SIMD) by 9%.
 template <int D>
-constexpr int kDkdvGroups = D == 64 ? 2 : 1;
+constexpr int kDkdvGroups = 2;
 template <int D>
 constexpr int kDqGroups = 2;
 
@@ -608,7 +633,10 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
     return !(e && e[0] == '0');
   }();
   bool launched = false;
-  if constexpr (GK == 2 && GQ == 2) {   // D = 64: both kernels take 8 waves
+  // One launch where it pays (measured): at D = 64 always, at D = 128 for
+  // causal heads (B1 H8 N4096: 0.255 -> 0.186 ms), not for non-causal ones
+  // (B4 H16 N4096: 2.36 -> 2.50 ms), whose units are all the same length.
+  if constexpr (GK == 2 && GQ == 2 && (D == 64 || CAUSAL)) {
     if (fused) {
       hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
                          s, Q, K, V, G, nl, di, dk_q, dv_q, dq, geo, nb, total, c, scale);
