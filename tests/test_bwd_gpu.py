@@ -136,7 +136,7 @@ def test_fp16_inputs_and_forward_outputs(fa, dev):
     _compare([t.cpu().numpy() for t in (dQ, dK, dV)], ref, TIGHT_ATOL, TIGHT_RTOL, "fp16")
 
 
-@pytest.mark.parametrize("D,causal", [(64, False), (64, True), (128, False)])
+@pytest.mark.parametrize("D,causal", [(64, False), (64, True), (128, False), (128, True)])
 def test_headline_shape(fa, dev, D, causal):
     """B1 H8 N4096: two heads against the oracle, every head through identities.
 
