@@ -130,7 +130,10 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
     pages = (ctx + 15) // 16
     other = float(pages.sum() * 4 + B * H * D * 2 * 2 + B * H * 4)
     alg = kv_bytes + other
-    del kp, vp
+    # The same pools and query in bf16 (same bytes).
+    kb, vb, qb = kp.bfloat16(), vp.bfloat16(), q.bfloat16()
+    ms_bf16 = median_of(lambda: fa.decode_paged(qb, kb, vb, tt, tc, S), reps, 3, iters, torch)
+    del kb, vb, kp, vp
     # GQA: the same contexts with 8 KV heads shared by groups of 4 query heads.
     # Bytes count each KV page once (what a group-aware kernel must read).
     Hkv = 8
@@ -149,6 +152,8 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
         "split_pass_GBps": round(alg / (ms_split * 1e-3) / 1e9, 1),
         "gqa_H32_Hkv8": {"ms": round(ms_gqa, 5), "algorithmic_bytes": alg_gqa,
                          "GBps_unique_kv": round(alg_gqa / (ms_gqa * 1e-3) / 1e9, 1)},
+        "bf16": {"ms": round(ms_bf16, 5), "GBps": round(alg / (ms_bf16 * 1e-3) / 1e9, 1),
+                 "pct_hbm_peak": round(100 * alg / (ms_bf16 * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)},
     }
 
 

@@ -99,7 +99,8 @@ def backward_varlen(q, k, v, o, dO, L, cu_seqlens, max_seqlen: int, causal: bool
 
 
 def kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens=None):
-    """Write k_new/v_new [B,H,T,D] into the pools at start_pos[b] + t, in place.
+    """Write k_new/v_new [B,H,T,D] into the pools at start_pos[b] + t, in place
+    (all four fp16, or all four bf16).
 
     Returns bad int32 [B]: 1 where a token of the sequence had no valid page
     (that token is not written).
@@ -108,7 +109,10 @@ def kv_append(k_new, v_new, k_pool, v_pool, page_table, start_pos, new_lens=None
 
 
 def decode_paged(q, k_pool, v_pool, page_table, ctx_lens, num_splits: int = 16):
-    """[O, L] of one query token per sequence over its paged K/V (split pass + combine)."""
+    """[O, L] of one query token per sequence over its paged K/V (split pass + combine).
+
+    q and the pools are all fp16 or all bf16; O has q's dtype, L is fp32.
+    """
     return _C.decode_paged(q, k_pool, v_pool, page_table, ctx_lens, num_splits)
 
 

@@ -44,8 +44,10 @@ SIGNATURES = {
     "fa_validate_fwd_varlen": (C.c_int, [_vp] * 5 + [_i64] * 6),
     "fa_fwd_varlen_f16": (C.c_int, [_vp] * 6 + [_i64] * 6 + [C.c_int, _vp]),
     "fa_decode_paged_gqa_f16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 5),
+    "fa_decode_paged_bf16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 5),
     "fa_validate_kv_append": (C.c_int, [_vp] * 8 + [_i64] * 7),
     "fa_kv_append_f16": (C.c_int, [_vp] * 8 + [_i64] * 7 + [_vp]),
+    "fa_kv_append_bf16": (C.c_int, [_vp] * 8 + [_i64] * 7 + [_vp]),
     "fa_bwd_gqa_workspace_floats": (_i64, [_i64] * 5),
     "fa_bwd_gqa_f16": (C.c_int, [_vp] * 10 + [_i64] * 5 + [C.c_int, _vp]),
     "fa_bwd_bf16": (C.c_int, [_vp] * 10 + [_i64] * 5 + [C.c_int, _vp]),

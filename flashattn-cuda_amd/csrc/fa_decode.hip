@@ -5,7 +5,7 @@
 // page table, computed per (sequence, head, split) as a normalised partial
 // (O_s, L_s), then merged by L = log sum_s exp(L_s), O = sum_s exp(L_s - L) O_s.
 //
-// Pool layout: [num_pages, H_kv, 16, D] fp16 (H_kv = H, or fewer KV heads
+// Pool layout: [num_pages, H_kv, 16, D] fp16 or bf16 (H_kv = H, or fewer KV heads
 // shared by groups of H / H_kv query heads), so the 16 tokens of one head in a
 // page are 16*D*2 contiguous bytes (4 KiB at D=128): one wave reads a page of
 // one head as fully coalesced 16-byte loads.
@@ -28,13 +28,40 @@ constexpr int kPage = 16;
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / 64;
 
-template <int D>
+// Element types of q, the pools and O: fp16, or bf16 (BF16 = true). Products
+// of two 16-bit values are exact in fp32; the dot product accumulates in fp32
+// (v_dot2_f32_f16 / v_dot2_f32_bf16) and everything after it is fp32.
+template <bool BF16>
+struct DecT {
+  using e = f16;
+  using v8 = f16x8;
+  using v2 = f16x2;
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
+};
+template <>
+struct DecT<true> {
+  using e = __bf16;
+  using v8 = bf16x8;
+  using v2 = bf16x2;
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
+
+template <int D, bool BF16>
 __global__ void __launch_bounds__(kDecThreads)
-fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
-                       const f16* __restrict__ vpool, const int32_t* __restrict__ page_table,
+fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
+                       const typename DecT<BF16>::e* __restrict__ kpool,
+                       const typename DecT<BF16>::e* __restrict__ vpool,
+                       const int32_t* __restrict__ page_table,
                        const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
                        float* __restrict__ part_lse, int H, int Hkv, int max_pages, int num_pages,
                        int S, float c) {
+  using T = DecT<BF16>;
+  using v8 = typename T::v8;
+  using v2 = typename T::v2;
   constexpr int DPL = D / 4;   // d per lane
   constexpr int NV = DPL / 8;  // 16-byte vectors per lane per row
   __shared__ float sh_o[kDecWaves][D];
@@ -59,14 +86,14 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
   const int p0 = min(s * chunk, pages);
   const int p1 = min(p0 + chunk, pages);
 
-  // Query slice of this lane as fp16 pairs.
-  const f16* qp = q + ((size_t)b * H + h) * D + dq * DPL;
-  f16x2 qv[DPL / 2];
+  // Query slice of this lane as element pairs.
+  const typename T::e* qp = q + ((size_t)b * H + h) * D + dq * DPL;
+  v2 qv[DPL / 2];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    f16x8 x = *reinterpret_cast<const f16x8*>(qp + 8 * i);
+    v8 x = *reinterpret_cast<const v8*>(qp + 8 * i);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) qv[4 * i + e] = f16x2{x[2 * e], x[2 * e + 1]};
+    for (int e = 0; e < 4; ++e) qv[4 * i + e] = v2{x[2 * e], x[2 * e + 1]};
   }
 
   float m = -INFINITY, l = 0.f;
@@ -78,7 +105,7 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
   const int kvh = h / (H / Hkv);
   // The wave's next page is loaded into (kn, vn) before the current one is
   // used, so one page per wave is always in flight behind the arithmetic.
-  f16x8 kn[NV], vn[NV];
+  v8 kn[NV], vn[NV];
   bool ok_n = false;
   auto load_page = [&](int p) {
     const int pid = pt[p];
@@ -86,13 +113,13 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
     if (!ok_n) return;
     const size_t base = ((size_t)pid * Hkv + kvh) * (kPage * D) + (size_t)tok * D + dq * DPL;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) kn[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
+    for (int i = 0; i < NV; ++i) kn[i] = *reinterpret_cast<const v8*>(kpool + base + 8 * i);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) vn[i] = *reinterpret_cast<const f16x8*>(vpool + base + 8 * i);
+    for (int i = 0; i < NV; ++i) vn[i] = *reinterpret_cast<const v8*>(vpool + base + 8 * i);
   };
   if (p0 + wave < p1) load_page(p0 + wave);
   for (int p = p0 + wave; p < p1; p += kDecWaves) {
-    f16x8 kv[NV], vv[NV];
+    v8 kv[NV], vv[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       kv[i] = kn[i];
@@ -106,7 +133,7 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
     for (int i = 0; i < NV; ++i) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        dot = __builtin_amdgcn_fdot2(qv[4 * i + e], f16x2{kv[i][2 * e], kv[i][2 * e + 1]}, dot, false);
+        dot = T::dot2(qv[4 * i + e], v2{kv[i][2 * e], kv[i][2 * e + 1]}, dot);
       }
     }
     dot += __shfl_xor(dot, 1, 64);
@@ -172,13 +199,18 @@ fa_decode_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
 // used for all G heads (a lane's dot products, softmax state and output
 // slice are kept per head), so a page is read once per KV head instead of
 // once per query head. Waves split the pages as above and merge per head.
-template <int D, int G>
+template <int D, int G, bool BF16>
 __global__ void __launch_bounds__(kDecThreads)
-fa_decode_split_group_kernel(const f16* __restrict__ q, const f16* __restrict__ kpool,
-                             const f16* __restrict__ vpool, const int32_t* __restrict__ page_table,
+fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
+                             const typename DecT<BF16>::e* __restrict__ kpool,
+                             const typename DecT<BF16>::e* __restrict__ vpool,
+                             const int32_t* __restrict__ page_table,
                              const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
                              float* __restrict__ part_lse, int H, int Hkv, int max_pages,
                              int num_pages, int S, float c) {
+  using T = DecT<BF16>;
+  using v8 = typename T::v8;
+  using v2 = typename T::v2;
   constexpr int DPL = D / 4;   // d per lane
   constexpr int NV = DPL / 8;  // 16-byte vectors per lane per row
   __shared__ float sh_o[kDecWaves][G][D];
@@ -205,15 +237,15 @@ fa_decode_split_group_kernel(const f16* __restrict__ q, const f16* __restrict__ 
   const int p0 = min(s * chunk, pages);
   const int p1 = min(p0 + chunk, pages);
 
-  f16x2 qv[G][DPL / 2];
+  v2 qv[G][DPL / 2];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const f16* qp = q + ((size_t)b * H + h0 + g) * D + dq * DPL;
+    const typename T::e* qp = q + ((size_t)b * H + h0 + g) * D + dq * DPL;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      f16x8 x = *reinterpret_cast<const f16x8*>(qp + 8 * i);
+      v8 x = *reinterpret_cast<const v8*>(qp + 8 * i);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qv[g][4 * i + e] = f16x2{x[2 * e], x[2 * e + 1]};
+      for (int e = 0; e < 4; ++e) qv[g][4 * i + e] = v2{x[2 * e], x[2 * e + 1]};
     }
   }
 
@@ -232,11 +264,11 @@ fa_decode_split_group_kernel(const f16* __restrict__ q, const f16* __restrict__ 
     const int pid = pt[p];
     if (pid < 0 || pid >= num_pages) { bad = true; continue; }
     const size_t base = ((size_t)pid * Hkv + hk) * (kPage * D) + (size_t)tok * D + dq * DPL;
-    f16x8 kv[NV], vv[NV];
+    v8 kv[NV], vv[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const f16x8*>(kpool + base + 8 * i);
+    for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const v8*>(kpool + base + 8 * i);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const f16x8*>(vpool + base + 8 * i);
+    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const v8*>(vpool + base + 8 * i);
     const bool live = p * kPage + tok < ctx;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -245,8 +277,7 @@ fa_decode_split_group_kernel(const f16* __restrict__ q, const f16* __restrict__ 
       for (int i = 0; i < NV; ++i) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          dot = __builtin_amdgcn_fdot2(qv[g][4 * i + e], f16x2{kv[i][2 * e], kv[i][2 * e + 1]}, dot,
-                                       false);
+          dot = T::dot2(qv[g][4 * i + e], v2{kv[i][2 * e], kv[i][2 * e + 1]}, dot);
         }
       }
       dot += __shfl_xor(dot, 1, 64);
@@ -315,10 +346,10 @@ fa_decode_split_group_kernel(const f16* __restrict__ q, const f16* __restrict__ 
 }
 
 // One workgroup of D threads per (b, h): thread d merges column d.
-template <int D>
+template <int D, bool BF16>
 __global__ void __launch_bounds__(D)
 fa_lse_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse,
-                      f16* __restrict__ o, float* __restrict__ lse, int S) {
+                      typename DecT<BF16>::e* __restrict__ o, float* __restrict__ lse, int S) {
   const int bh = blockIdx.x;
   const int d = threadIdx.x;
   const float* ls = part_lse + (size_t)bh * S;
@@ -348,7 +379,7 @@ fa_lse_combine_kernel(const float* __restrict__ part_o, const float* __restrict_
     }
     out = acc;
   }
-  o[(size_t)bh * D + d] = (f16)out;
+  o[(size_t)bh * D + d] = (typename DecT<BF16>::e)out;
   if (lse != nullptr && d == 0) lse[bh] = L;
 }
 
@@ -357,13 +388,18 @@ fa_lse_combine_kernel(const float* __restrict__ part_o, const float* __restrict_
 namespace fa {
 // Split pass with query heads h reading pool head h / (H / Hkv); arguments
 // already validated.
+template <bool BF16>
 static int decode_split(const void* q, const void* k_pool, const void* v_pool,
                         const int32_t* page_table, const int32_t* ctx_lens, int64_t B, int64_t H,
                         int64_t Hkv, int64_t D, int64_t max_pages, int64_t num_pages,
                         int64_t num_splits, float* part_o, float* part_lse, void* stream) {
+  using E = typename DecT<BF16>::e;
   if (!part_o || !part_lse) return FA_ERR_NULL_POINTER;
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const E* Q = (const E*)q;
+  const E* Kp = (const E*)k_pool;
+  const E* Vp = (const E*)v_pool;
   // Grouped KV heads: G query heads per workgroup share each page read. At
   // D = 128 four heads' state needs 256 VGPRs (one wave per SIMD, too few to
   // stream HBM), so G stays at 2 there (measured: group-of-4 pools at 507 µs
@@ -373,11 +409,10 @@ static int decode_split(const void* q, const void* k_pool, const void* v_pool,
   const int G = (group % 4 == 0 && maxg >= 4) ? 4 : (group % 2 == 0 ? 2 : 1);
   if (G > 1) {
     const dim3 ggrid((unsigned)num_splits, (unsigned)(H / G), (unsigned)B);
-#define FA_DEC_GROUP(DD, GG)                                                                      \
-  hipLaunchKernelGGL((fa_decode_split_group_kernel<DD, GG>), ggrid, dim3(kDecThreads), 0, s,       \
-                     (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table, ctx_lens, \
-                     part_o, part_lse, (int)H, (int)Hkv, (int)max_pages, (int)num_pages,           \
-                     (int)num_splits, c)
+#define FA_DEC_GROUP(DD, GG)                                                                    \
+  hipLaunchKernelGGL((fa_decode_split_group_kernel<DD, GG, BF16>), ggrid, dim3(kDecThreads), 0, \
+                     s, Q, Kp, Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,     \
+                     (int)max_pages, (int)num_pages, (int)num_splits, c)
     if (D == 128) {
       FA_DEC_GROUP(128, 2);
     } else {
@@ -389,15 +424,36 @@ static int decode_split(const void* q, const void* k_pool, const void* v_pool,
   }
   dim3 grid((unsigned)num_splits, (unsigned)H, (unsigned)B);
   if (D == 128) {
-    hipLaunchKernelGGL((fa_decode_split_kernel<128>), grid, dim3(kDecThreads), 0, s,
-                       (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table,
-                       ctx_lens, part_o, part_lse, (int)H, (int)Hkv, (int)max_pages,
-                       (int)num_pages, (int)num_splits, c);
+    hipLaunchKernelGGL((fa_decode_split_kernel<128, BF16>), grid, dim3(kDecThreads), 0, s, Q, Kp,
+                       Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,
+                       (int)max_pages, (int)num_pages, (int)num_splits, c);
   } else {
-    hipLaunchKernelGGL((fa_decode_split_kernel<64>), grid, dim3(kDecThreads), 0, s,
-                       (const f16*)q, (const f16*)k_pool, (const f16*)v_pool, page_table,
-                       ctx_lens, part_o, part_lse, (int)H, (int)Hkv, (int)max_pages,
-                       (int)num_pages, (int)num_splits, c);
+    hipLaunchKernelGGL((fa_decode_split_kernel<64, BF16>), grid, dim3(kDecThreads), 0, s, Q, Kp,
+                       Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,
+                       (int)max_pages, (int)num_pages, (int)num_splits, c);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FA_OK : -(int)e;
+}
+
+// LSE combine of [B, H, num_splits] partials into O [B, H, D] (fp16 or bf16)
+// and L fp32 [B, H] (may be null).
+template <bool BF16>
+static int lse_combine(const float* part_o, const float* part_lse, int64_t B, int64_t H,
+                       int64_t D, int64_t num_splits, void* o, float* lse, void* stream) {
+  using E = typename DecT<BF16>::e;
+  if (!part_o || !part_lse || !o) return FA_ERR_NULL_POINTER;
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
+  if (num_splits < 1 || num_splits > 16) return FA_ERR_NUM_SPLITS;
+  if (B * H > (int64_t(1) << 31) - 1) return FA_ERR_TOO_LARGE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (D == 128) {
+    hipLaunchKernelGGL((fa_lse_combine_kernel<128, BF16>), dim3((unsigned)(B * H)), dim3(128), 0,
+                       s, part_o, part_lse, (E*)o, lse, (int)num_splits);
+  } else {
+    hipLaunchKernelGGL((fa_lse_combine_kernel<64, BF16>), dim3((unsigned)(B * H)), dim3(64), 0,
+                       s, part_o, part_lse, (E*)o, lse, (int)num_splits);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? FA_OK : -(int)e;
@@ -412,29 +468,14 @@ extern "C" int fa_decode_split_f16(const void* q, const void* k_pool, const void
   int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
                               max_pages, num_pages, num_splits);
   if (st != FA_OK) return st;
-  return fa::decode_split(q, k_pool, v_pool, page_table, ctx_lens, B, H, H, D, max_pages,
-                          num_pages, num_splits, part_o, part_lse, stream);
+  return fa::decode_split<false>(q, k_pool, v_pool, page_table, ctx_lens, B, H, H, D, max_pages,
+                                 num_pages, num_splits, part_o, part_lse, stream);
 }
 
 extern "C" int fa_lse_combine_f32(const float* part_o, const float* part_lse, int64_t B,
                                   int64_t H, int64_t D, int64_t num_splits, void* o,
                                   float* lse, void* stream) {
-  using namespace fa;
-  if (!part_o || !part_lse || !o) return FA_ERR_NULL_POINTER;
-  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
-  if (B <= 0 || H <= 0) return FA_ERR_BATCH_HEADS;
-  if (num_splits < 1 || num_splits > 16) return FA_ERR_NUM_SPLITS;
-  if (B * H > (int64_t(1) << 31) - 1) return FA_ERR_TOO_LARGE;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (D == 128) {
-    hipLaunchKernelGGL((fa_lse_combine_kernel<128>), dim3((unsigned)(B * H)), dim3(128), 0, s,
-                       part_o, part_lse, (f16*)o, lse, (int)num_splits);
-  } else {
-    hipLaunchKernelGGL((fa_lse_combine_kernel<64>), dim3((unsigned)(B * H)), dim3(64), 0, s,
-                       part_o, part_lse, (f16*)o, lse, (int)num_splits);
-  }
-  hipError_t e = hipGetLastError();
-  return e == hipSuccess ? FA_OK : -(int)e;
+  return fa::lse_combine<false>(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
 }
 
 extern "C" int fa_decode_paged_f16(const void* q, const void* k_pool, const void* v_pool,
@@ -449,18 +490,42 @@ extern "C" int fa_decode_paged_f16(const void* q, const void* k_pool, const void
   return fa_lse_combine_f32(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
 }
 
+namespace fa {
+template <bool BF16>
+static int decode_paged_gqa(const void* q, const void* k_pool, const void* v_pool,
+                            const int32_t* page_table, const int32_t* ctx_lens, int64_t B,
+                            int64_t H, int64_t H_kv, int64_t D, int64_t page_size,
+                            int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                            float* part_o, float* part_lse, void* o, float* lse, void* stream) {
+  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
+                              max_pages, num_pages, num_splits);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  st = decode_split<BF16>(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D, max_pages,
+                          num_pages, num_splits, part_o, part_lse, stream);
+  if (st != FA_OK) return st;
+  return lse_combine<BF16>(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
+}
+}  // namespace fa
+
 extern "C" int fa_decode_paged_gqa_f16(const void* q, const void* k_pool, const void* v_pool,
                                        const int32_t* page_table, const int32_t* ctx_lens,
                                        int64_t B, int64_t H, int64_t H_kv, int64_t D,
                                        int64_t page_size, int64_t max_pages, int64_t num_pages,
                                        int64_t num_splits, float* part_o, float* part_lse,
                                        void* o, float* lse, void* stream) {
-  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
-                              max_pages, num_pages, num_splits);
-  if (st != FA_OK) return st;
-  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
-  st = fa::decode_split(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D, max_pages,
-                        num_pages, num_splits, part_o, part_lse, stream);
-  if (st != FA_OK) return st;
-  return fa_lse_combine_f32(part_o, part_lse, B, H, D, num_splits, o, lse, stream);
+  return fa::decode_paged_gqa<false>(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D,
+                                     page_size, max_pages, num_pages, num_splits, part_o,
+                                     part_lse, o, lse, stream);
+}
+
+extern "C" int fa_decode_paged_bf16(const void* q, const void* k_pool, const void* v_pool,
+                                    const int32_t* page_table, const int32_t* ctx_lens,
+                                    int64_t B, int64_t H, int64_t H_kv, int64_t D,
+                                    int64_t page_size, int64_t max_pages, int64_t num_pages,
+                                    int64_t num_splits, float* part_o, float* part_lse, void* o,
+                                    float* lse, void* stream) {
+  return fa::decode_paged_gqa<true>(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D,
+                                    page_size, max_pages, num_pages, num_splits, part_o,
+                                    part_lse, o, lse, stream);
 }

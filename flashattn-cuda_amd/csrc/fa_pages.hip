@@ -83,3 +83,14 @@ extern "C" int fa_kv_append_f16(const void* k_new, const void* v_new, const int3
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FA_OK : -(int)e;
 }
+
+// bf16 rows into bf16 pools: the kernel moves 16-byte chunks of 16-bit
+// elements without arithmetic, so the fp16 path serves both element types.
+extern "C" int fa_kv_append_bf16(const void* k_new, const void* v_new, const int32_t* page_table,
+                                 const int32_t* start_pos, const int32_t* new_lens, void* k_pool,
+                                 void* v_pool, int32_t* bad, int64_t B, int64_t H, int64_t T,
+                                 int64_t D, int64_t page_size, int64_t max_pages,
+                                 int64_t num_pages, void* stream) {
+  return fa_kv_append_f16(k_new, v_new, page_table, start_pos, new_lens, k_pool, v_pool, bad, B,
+                          H, T, D, page_size, max_pages, num_pages, stream);
+}

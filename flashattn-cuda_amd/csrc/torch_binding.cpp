@@ -316,9 +316,10 @@ DecodeArgs check_decode(const torch::Tensor& q, const torch::Tensor& k_pool,
   TORCH_CHECK(q.dim() == 3, "q must be 3D [B, H, D]");
   TORCH_CHECK(k_pool.dim() == 4, "k_pool must be 4D [num_pages, H, page_size, D]");
   TORCH_CHECK(v_pool.sizes() == k_pool.sizes(), "v_pool must have the same shape as k_pool");
-  TORCH_CHECK(q.scalar_type() == torch::kHalf && k_pool.scalar_type() == torch::kHalf &&
-                  v_pool.scalar_type() == torch::kHalf,
-              "q/k_pool/v_pool must be float16");
+  TORCH_CHECK((q.scalar_type() == torch::kHalf || q.scalar_type() == torch::kBFloat16) &&
+                  k_pool.scalar_type() == q.scalar_type() &&
+                  v_pool.scalar_type() == q.scalar_type(),
+              "q/k_pool/v_pool must be all float16 or all bfloat16");
   TORCH_CHECK(page_table.dim() == 2 && page_table.scalar_type() == torch::kInt,
               "page_table must be int32 [B, max_pages]");
   TORCH_CHECK(ctx_lens.dim() == 1 && ctx_lens.scalar_type() == torch::kInt,
@@ -350,6 +351,8 @@ std::vector<torch::Tensor> decode_partials(torch::Tensor q, torch::Tensor k_pool
                                            torch::Tensor ctx_lens, int64_t num_splits) {
   const DecodeArgs a = check_decode(q, k_pool, v_pool, page_table, ctx_lens);
   TORCH_CHECK(a.Hkv == a.H, "decode_partials takes pools with H heads (use decode_paged for GQA)");
+  TORCH_CHECK(q.scalar_type() == torch::kHalf,
+              "decode_partials takes float16 (use decode_paged for bfloat16)");
   const c10::DeviceGuard guard(q.device());
   auto part_o = torch::empty({a.B, a.H, num_splits, a.D}, q.options().dtype(torch::kFloat));
   auto part_lse = torch::empty({a.B, a.H, num_splits}, q.options().dtype(torch::kFloat));
@@ -392,13 +395,14 @@ std::vector<torch::Tensor> decode_paged(torch::Tensor q, torch::Tensor k_pool, t
   float* part_lse = part_o + a.B * a.H * num_splits * a.D;
   auto o = torch::empty({a.B, a.H, a.D}, q.options());
   auto lse = torch::empty({a.B, a.H}, q.options().dtype(torch::kFloat));
-  const int st = fa_decode_paged_gqa_f16(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
-                                         page_table.data_ptr<int32_t>(),
-                                         ctx_lens.data_ptr<int32_t>(), a.B, a.H, a.Hkv, a.D,
-                                         a.page_size, a.max_pages, a.num_pages, num_splits, part_o,
-                                         part_lse, o.data_ptr(), lse.data_ptr<float>(),
-                                         current_stream(q));
-  check_status(st, "fa_decode_paged_gqa_f16");
+  // O takes q's element type (fp16 or bf16).
+  const bool bf16 = q.scalar_type() == torch::kBFloat16;
+  const auto fn = bf16 ? fa_decode_paged_bf16 : fa_decode_paged_gqa_f16;
+  const int st = fn(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                    page_table.data_ptr<int32_t>(), ctx_lens.data_ptr<int32_t>(), a.B, a.H, a.Hkv,
+                    a.D, a.page_size, a.max_pages, a.num_pages, num_splits, part_o, part_lse,
+                    o.data_ptr(), lse.data_ptr<float>(), current_stream(q));
+  check_status(st, bf16 ? "fa_decode_paged_bf16" : "fa_decode_paged_gqa_f16");
   return {o, lse};
 }
 
@@ -415,9 +419,11 @@ torch::Tensor kv_append(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor 
               "k_new and v_new must be [B, H, T, D] of the same shape");
   TORCH_CHECK(k_pool.dim() == 4 && v_pool.sizes() == k_pool.sizes(),
               "k_pool and v_pool must be [num_pages, H, page_size, D] of the same shape");
-  TORCH_CHECK(k_new.scalar_type() == torch::kHalf && v_new.scalar_type() == torch::kHalf &&
-                  k_pool.scalar_type() == torch::kHalf && v_pool.scalar_type() == torch::kHalf,
-              "k_new/v_new/k_pool/v_pool must be float16");
+  TORCH_CHECK((k_new.scalar_type() == torch::kHalf || k_new.scalar_type() == torch::kBFloat16) &&
+                  v_new.scalar_type() == k_new.scalar_type() &&
+                  k_pool.scalar_type() == k_new.scalar_type() &&
+                  v_pool.scalar_type() == k_new.scalar_type(),
+              "k_new/v_new/k_pool/v_pool must be all float16 or all bfloat16");
   const int64_t B = k_new.size(0), H = k_new.size(1), T = k_new.size(2), D = k_new.size(3);
   TORCH_CHECK(k_pool.size(1) == H && k_pool.size(3) == D,
               "k_pool must be [num_pages, H, page_size, D] with k_new's H and D");
@@ -446,12 +452,13 @@ torch::Tensor kv_append(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor 
               "kv_append tensors must be on the same device");
   const c10::DeviceGuard guard(dev);
   auto bad = torch::zeros({B}, page_table.options());
-  const int st = fa_kv_append_f16(k_new.data_ptr(), v_new.data_ptr(),
-                                  page_table.data_ptr<int32_t>(), start_pos.data_ptr<int32_t>(),
-                                  lens, k_pool.data_ptr(), v_pool.data_ptr(),
-                                  bad.data_ptr<int32_t>(), B, H, T, D, k_pool.size(2),
-                                  page_table.size(1), k_pool.size(0), current_stream(k_new));
-  check_status(st, "fa_kv_append_f16");
+  const bool bf16 = k_new.scalar_type() == torch::kBFloat16;
+  const auto fn = bf16 ? fa_kv_append_bf16 : fa_kv_append_f16;
+  const int st = fn(k_new.data_ptr(), v_new.data_ptr(), page_table.data_ptr<int32_t>(),
+                    start_pos.data_ptr<int32_t>(), lens, k_pool.data_ptr(), v_pool.data_ptr(),
+                    bad.data_ptr<int32_t>(), B, H, T, D, k_pool.size(2), page_table.size(1),
+                    k_pool.size(0), current_stream(k_new));
+  check_status(st, bf16 ? "fa_kv_append_bf16" : "fa_kv_append_f16");
   return bad;
 }
 
@@ -545,7 +552,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("kv_append", &kv_append, "write new K/V rows into the paged pools; returns bad [B]",
         py::arg("k_new"), py::arg("v_new"), py::arg("k_pool"), py::arg("v_pool"),
         py::arg("page_table"), py::arg("start_pos"), py::arg("new_lens") = py::none());
-  m.def("decode_paged", &decode_paged, "split-KV paged decode: returns [O half, L float]",
+  m.def("decode_paged", &decode_paged, "split-KV paged decode (fp16 or bf16): returns [O in q's dtype, L float]",
         py::arg("q"), py::arg("k_pool"), py::arg("v_pool"), py::arg("page_table"),
         py::arg("ctx_lens"), py::arg("num_splits") = 16);
   m.def("decode_partials", &decode_partials, "split pass only: returns [part_o, part_lse]",

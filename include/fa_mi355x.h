@@ -282,6 +282,18 @@ int fa_decode_paged_gqa_f16(const void* q, const void* k_pool, const void* v_poo
                             float* part_o, float* part_lse, void* o, float* lse, void* stream);
 
 /*
+ * fa_decode_paged_gqa_f16 for bf16 q, pools and O (same layouts and
+ * arguments; QK dot products in fp32 from bf16 pairs, softmax and merges in
+ * fp32, O rounded to bf16 to nearest even). No reference counterpart (the
+ * reference has neither a decode path nor bf16).
+ */
+int fa_decode_paged_bf16(const void* q, const void* k_pool, const void* v_pool,
+                         const int32_t* page_table, const int32_t* ctx_lens, int64_t B, int64_t H,
+                         int64_t H_kv, int64_t D, int64_t page_size, int64_t max_pages,
+                         int64_t num_pages, int64_t num_splits, float* part_o, float* part_lse,
+                         void* o, float* lse, void* stream);
+
+/*
  * Host-only argument check of fa_kv_append_f16. No reference counterpart.
  */
 int fa_validate_kv_append(const void* k_new, const void* v_new, const int32_t* page_table,
@@ -309,6 +321,15 @@ int fa_kv_append_f16(const void* k_new, const void* v_new, const int32_t* page_t
                      const int32_t* start_pos, const int32_t* new_lens, void* k_pool,
                      void* v_pool, int32_t* bad, int64_t B, int64_t H, int64_t T, int64_t D,
                      int64_t page_size, int64_t max_pages, int64_t num_pages, void* stream);
+
+/*
+ * fa_kv_append_f16 for bf16 rows and pools (same arguments; the copy moves
+ * 16-bit elements without arithmetic). No reference counterpart.
+ */
+int fa_kv_append_bf16(const void* k_new, const void* v_new, const int32_t* page_table,
+                      const int32_t* start_pos, const int32_t* new_lens, void* k_pool,
+                      void* v_pool, int32_t* bad, int64_t B, int64_t H, int64_t T, int64_t D,
+                      int64_t page_size, int64_t max_pages, int64_t num_pages, void* stream);
 
 #ifdef __cplusplus
 }

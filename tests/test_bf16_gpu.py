@@ -1,4 +1,6 @@
-"""GPU tier: the bfloat16 forward (forward_bf16) against the CPU oracle.
+"""GPU tier: the bfloat16 paths against the CPU oracle: forward (forward_bf16),
+backward (backward_bf16), paged decode and page writer (decode_paged and
+kv_append with bf16 tensors).
 
 The oracle runs fp32 math on the bf16-rounded inputs (oracle.bf16_cast, pinned
 against torch's conversion). Tolerances, written out:
@@ -14,7 +16,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import bf16_cast, naive_attention, naive_attention_backward
+from oracle import (append_pages, bf16_cast, decode_attention, naive_attention,
+                    naive_attention_backward)
 
 pytestmark = pytest.mark.gpu
 
@@ -130,3 +133,118 @@ def test_bf16_backward_matches_fp16_path_closely(fa, dev):
     gh = fa.backward(tq, tk, tv, Oh, tg, Lh, causal=True)
     for a, b in zip(gb, gh):
         assert (a - b).abs().max().item() <= 4e-2
+
+
+# ---- paged decode and page writer with bf16 q and pools ----
+
+def _pages(rng, B, ctx, Hkv, D, extra=2):
+    """Page table (a permutation of the pool's pages) and fp32 pools."""
+    pages = [(c + 15) // 16 for c in ctx]
+    P = sum(pages) + extra
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((B, max(max(pages), 1)), np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    kp = rng.standard_normal((P, Hkv, 16, D)).astype(np.float32)
+    vp = rng.standard_normal((P, Hkv, 16, D)).astype(np.float32)
+    return table, kp, vp
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hkv", [4, 2, 1])
+@pytest.mark.parametrize("S", [1, 3, 16])
+def test_bf16_decode_vs_oracle(fa, dev, D, Hkv, S):
+    """decode_paged with bf16 q and pools. The QK products of bf16 pairs are
+    exact in fp32 and P and V stay fp32, so only O's final rounding to bf16
+    separates it from the fp32 oracle on the bf16-rounded inputs:
+    |O - O_ref| <= 1e-3 + half a bf16 ulp of O_ref; L relative <= 1e-4."""
+    B, H = 5, 4
+    ctx = [1, 15, 16, 17, 300]
+    rng = np.random.default_rng(D + 10 * Hkv + S)
+    table, kp, vp = _pages(rng, B, ctx, Hkv, D)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    bf = lambda x: torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    tt = torch.from_numpy(table).to(dev)
+    tc = torch.from_numpy(np.array(ctx, np.int32)).to(dev)
+    O, L = fa.decode_paged(bf(q), bf(kp), bf(vp), tt, tc, num_splits=S)
+    torch.cuda.synchronize()
+    assert O.dtype == torch.bfloat16 and L.dtype == torch.float32
+    g = H // Hkv
+    Or, Lr = decode_attention(bf16_cast(q), np.repeat(bf16_cast(kp), g, axis=1),
+                              np.repeat(bf16_cast(vp), g, axis=1), table, np.array(ctx))
+    err = np.abs(O.float().cpu().numpy() - Or)
+    assert (err <= 1e-3 + bf16_half_ulp(Or)).all(), f"O err {err.max():.3e}"
+    l_err = np.abs(L.cpu().numpy() - Lr) / np.maximum(np.abs(Lr), 1.0)
+    assert l_err.max() <= 1e-4, f"L rel {l_err.max():.3e}"
+
+
+def test_bf16_decode_matches_fp16_decode(fa, dev):
+    """Inputs with at most 7 significant bits are exact in both formats: the
+    two decodes form the same fp32 products, so L agrees to fp32 accumulation
+    rounding (relative 1e-5) and O to the bf16 output rounding."""
+    B, H, D = 3, 8, 128
+    ctx = [40, 513, 2000]
+    rng = np.random.default_rng(21)
+    table, kp, vp = _pages(rng, B, ctx, H, D)
+    q = rng.standard_normal((B, H, D))
+    q, kp, vp = (np.clip(np.round(x * 16), -63, 63).astype(np.float32) / 16 for x in (q, kp, vp))
+    tt = torch.from_numpy(table).to(dev)
+    tc = torch.from_numpy(np.array(ctx, np.int32)).to(dev)
+    to = lambda x, dt: torch.from_numpy(x).to(dev).to(dt)
+    Oh, Lh = fa.decode_paged(*(to(x, torch.float16) for x in (q, kp, vp)), tt, tc, num_splits=16)
+    Ob, Lb = fa.decode_paged(*(to(x, torch.bfloat16) for x in (q, kp, vp)), tt, tc, num_splits=16)
+    torch.cuda.synchronize()
+    Lh, Lb = Lh.cpu().numpy(), Lb.cpu().numpy()
+    assert (np.abs(Lh - Lb) / np.maximum(np.abs(Lh), 1.0)).max() <= 1e-5
+    Oh, Ob = Oh.float().cpu().numpy(), Ob.float().cpu().numpy()
+    assert (np.abs(Ob - Oh) <= 1e-3 + bf16_half_ulp(Oh)).all()
+
+
+def test_bf16_kv_append_bit_exact(fa, dev):
+    """bf16 rows land in bf16 pools bit for bit: the GPU pools, read as int16
+    bit patterns, equal the oracle's append on the same bit patterns; then a
+    decode over the appended pages matches the oracle."""
+    B, H, T, D = 3, 4, 40, 128
+    rng = np.random.default_rng(9)
+    start = np.array([0, 5, 17], np.int32)
+    max_pages = 4                                   # positions up to 56 < 64
+    P = B * max_pages + 2
+    table = rng.permutation(P)[:B * max_pages].astype(np.int32).reshape(B, max_pages)
+    bf = lambda x: torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    tkp = bf(rng.standard_normal((P, H, 16, D)).astype(np.float32))
+    tvp = bf(rng.standard_normal((P, H, 16, D)).astype(np.float32))
+    tkn = bf(rng.standard_normal((B, H, T, D)).astype(np.float32))
+    tvn = bf(rng.standard_normal((B, H, T, D)).astype(np.float32))
+    bits = lambda t: t.view(torch.int16).cpu().numpy()
+    want_k, want_v, want_bad = append_pages(bits(tkp), bits(tvp), table, start, bits(tkn),
+                                            bits(tvn))
+    tt = torch.from_numpy(table).to(dev)
+    bad = fa.kv_append(tkn, tvn, tkp, tvp, tt, torch.from_numpy(start).to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(bad.cpu().numpy(), want_bad)
+    assert np.array_equal(bits(tkp), want_k) and np.array_equal(bits(tvp), want_v)
+    ctx = start + T
+    tq = bf(rng.standard_normal((B, H, D)).astype(np.float32))
+    O, L = fa.decode_paged(tq, tkp, tvp, tt, torch.from_numpy(ctx).to(dev), num_splits=4)
+    torch.cuda.synchronize()
+    f32 = lambda t: t.float().cpu().numpy()
+    Or, Lr = decode_attention(f32(tq), f32(tkp), f32(tvp), table, ctx)
+    err = np.abs(f32(O) - Or)
+    assert (err <= 1e-3 + bf16_half_ulp(Or)).all(), f"O err {err.max():.3e}"
+    assert (np.abs(L.cpu().numpy() - Lr) / np.maximum(np.abs(Lr), 1.0)).max() <= 1e-4
+
+
+def test_bf16_decode_rejects_mixed_dtypes(fa, dev):
+    q = torch.zeros(1, 2, 64, device=dev, dtype=torch.bfloat16)
+    kp = torch.zeros(1, 2, 16, 64, device=dev, dtype=torch.float16)
+    tt = torch.zeros(1, 1, device=dev, dtype=torch.int32)
+    tc = torch.ones(1, device=dev, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="all float16 or all bfloat16"):
+        fa.decode_paged(q, kp, kp, tt, tc)
+    with pytest.raises(RuntimeError, match="decode_partials takes float16"):
+        fa.decode_partials(q, kp.bfloat16(), kp.bfloat16(), tt, tc)
+    with pytest.raises(RuntimeError, match="all float16 or all bfloat16"):
+        fa.kv_append(kp.bfloat16(), kp.bfloat16(), kp, kp, tt, torch.zeros(1, device=dev,
+                                                                            dtype=torch.int32))
