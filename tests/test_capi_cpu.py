@@ -275,3 +275,19 @@ def test_validate_bwd_varlen(capi):
     assert lib.fa_validate_bwd_varlen(*bad) == capi.STATUS["FA_ERR_SEQ_LEN"]
     # the entry point rejects before touching the device
     assert lib.fa_bwd_varlen_f16(*bad, 0, None) == capi.STATUS["FA_ERR_SEQ_LEN"]
+
+
+def test_bf16_decode_and_page_writer_reject_before_touching_the_device(capi):
+    """The bf16 entry points run the fp16 ones' checks first (no launch)."""
+    lib = capi.load()
+    args = list(_dec())
+    gqa = args[:7] + [5] + args[7:] + [A, A, A, None, None]     # H_kv 5 does not divide H
+    assert lib.fa_decode_paged_bf16(*gqa) == capi.STATUS["FA_ERR_KV_HEADS"]
+    bad_s = list(_dec(S=20))
+    gqa = bad_s[:7] + [bad_s[6]] + bad_s[7:] + [A, A, A, None, None]
+    assert lib.fa_decode_paged_bf16(*gqa) == capi.STATUS["FA_ERR_NUM_SPLITS"]
+    ok = list(_dec())
+    gqa = ok[:7] + [ok[6]] + ok[7:] + [0, A, A, None, None]      # no part_o
+    assert lib.fa_decode_paged_bf16(*gqa) == capi.STATUS["FA_ERR_NULL_POINTER"]
+    assert lib.fa_kv_append_bf16(*_kv(ps=8), None) == capi.STATUS["FA_ERR_PAGE_SIZE"]
+    assert lib.fa_kv_append_bf16(*_kv(T=0), None) == capi.STATUS["FA_OK"]   # no launch
