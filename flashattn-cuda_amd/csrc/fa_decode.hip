@@ -50,6 +50,32 @@ struct DecT<true> {
   }
 };
 
+// Longest sequence first: grid index z (the slowest-varying one, so low z
+// is dispatched first) takes the sequence of rank z by decreasing
+// context length, ties by index. The longest splits then start first and the
+// shortest fill the tail instead of a long sequence dispatched last running
+// alone. Ranks of B <= kDecThreads contexts are computed from a copy in LDS;
+// larger batches keep the identity order. Invalid (negative) lengths rank
+// like any other value and are flagged by the caller as before.
+__device__ __forceinline__ int sequence_of_rank(const int32_t* __restrict__ ctx_lens, int B, int z,
+                                                int* sh_ctx, int* sh_seq) {
+  if (B > kDecThreads) return z;
+  const int t = threadIdx.x;
+  if (t < B) sh_ctx[t] = ctx_lens[t];
+  __syncthreads();
+  if (t < B) {
+    const int c = sh_ctx[t];
+    int r = 0;
+    for (int j = 0; j < B; ++j) {
+      const int cj = sh_ctx[j];
+      r += (cj > c) || (cj == c && j < t);
+    }
+    if (r == z) *sh_seq = t;   // ranks are a permutation: exactly one writer
+  }
+  __syncthreads();
+  return *sh_seq;
+}
+
 template <int D, bool BF16>
 __global__ void __launch_bounds__(kDecThreads)
 fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
@@ -68,8 +94,11 @@ fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
   __shared__ float sh_m[kDecWaves];
   __shared__ float sh_l[kDecWaves];
   __shared__ int sh_bad;
+  __shared__ int sh_ctx[kDecThreads];
+  __shared__ int sh_seq;
 
-  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int s = blockIdx.x, h = blockIdx.y;
+  const int b = sequence_of_rank(ctx_lens, (int)gridDim.z, (int)blockIdx.z, sh_ctx, &sh_seq);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok = lane >> 2;   // token within the page
   const int dq = lane & 3;     // quarter of D
@@ -217,8 +246,11 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
   __shared__ float sh_m[kDecWaves][G];
   __shared__ float sh_l[kDecWaves][G];
   __shared__ int sh_bad;
+  __shared__ int sh_ctx[kDecThreads];
+  __shared__ int sh_seq;
 
-  const int s = blockIdx.x, hg = blockIdx.y, b = blockIdx.z;
+  const int s = blockIdx.x, hg = blockIdx.y;
+  const int b = sequence_of_rank(ctx_lens, (int)gridDim.z, (int)blockIdx.z, sh_ctx, &sh_seq);
   const int h0 = hg * G;                  // first query head of this workgroup
   const int hk = h0 / (H / Hkv);          // their KV head (G divides H / Hkv)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

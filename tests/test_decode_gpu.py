@@ -140,6 +140,37 @@ def test_split_count_invariance(fa, dev):
     assert torch.equal(po[:, :, 0].half(), O1)
 
 
+@pytest.mark.parametrize("B,Hkv", [(40, 4), (300, 4), (300, 2)])
+def test_sequence_order_is_a_permutation(fa, dev, B, Hkv):
+    """Workgroups take sequences longest first (ranked in the kernel for
+    B <= 256, identity order above): every sequence is still decoded exactly
+    once, repeated and zero lengths included, against the oracle."""
+    rng = np.random.default_rng(B + Hkv)
+    ctx = rng.integers(0, 60, B)
+    ctx[::7] = 33                                   # ties broken by index
+    ctx[3] = 0
+    H, D = 4, 64
+    pages = (ctx + 15) // 16
+    P = int(pages.sum()) + 1
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((B, max(int(pages.max()), 1)), np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    q = rng.standard_normal((B, H, D)).astype(np.float16)
+    kp = rng.standard_normal((P, Hkv, 16, D)).astype(np.float16)
+    vp = rng.standard_normal((P, Hkv, 16, D)).astype(np.float16)
+    O, L = fa.decode_paged(*_dev(dev, q, kp, vp, table, ctx.astype(np.int32)), num_splits=3)
+    g = H // Hkv
+    Or, Lr = decode_attention(q, np.repeat(kp, g, axis=1), np.repeat(vp, g, axis=1), table, ctx)
+    O, L = O.float().cpu().numpy(), L.cpu().numpy()
+    assert np.abs(O - Or).max() <= 2e-3, f"B{B} Hkv{Hkv} O {np.abs(O - Or).max():.3e}"
+    assert np.array_equal(np.isneginf(L), np.isneginf(Lr))   # the empty sequence
+    fin = np.isfinite(Lr)
+    assert (np.abs(L[fin] - Lr[fin]) / np.maximum(np.abs(Lr[fin]), 1.0)).max() <= 1e-4
+
+
 def test_bad_page_ids_give_nan_not_fault(fa, dev):
     """Out-of-range page ids and over-long contexts poison only their sequence."""
     q, kp, vp, table, ctx = _small(12, B=3, H=2, D=64, ctx=[20, 40, 30])
