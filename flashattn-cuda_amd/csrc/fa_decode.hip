@@ -168,7 +168,14 @@ fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
     dot += __shfl_xor(dot, 1, 64);
     dot += __shfl_xor(dot, 2, 64);
     float st = dot * c;
-    if (p * kPage + tok >= ctx) st = -INFINITY;
+    if (p * kPage + tok >= ctx) {
+      // A slot past the context holds whatever the pool held (NaN and Inf
+      // included): its score is -inf and its V row is dropped, since
+      // 0 * NaN would poison every lane after the shuffle sums.
+      st = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) vv[i] = v8{};
+    }
     float mp = st;
     mp = fmaxf(mp, __shfl_xor(mp, 4, 64));
     mp = fmaxf(mp, __shfl_xor(mp, 8, 64));
@@ -302,6 +309,10 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
 #pragma unroll
     for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const v8*>(vpool + base + 8 * i);
     const bool live = p * kPage + tok < ctx;
+    if (!live) {   // slot past the context: drop its V row (it may hold NaN or Inf)
+#pragma unroll
+      for (int i = 0; i < NV; ++i) vv[i] = v8{};
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float dot = 0.f;

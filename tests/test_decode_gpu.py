@@ -218,3 +218,42 @@ def test_config5_full_size(fa, dev):
         Or, Lr = naive_attention(qb[None, None, None], kb[None, None], vb[None, None])
         Or, Lr = Or[:, :, 0], Lr[:, :, 0]
         _check(O[b:b + 1, h:h + 1], L[b:b + 1, h:h + 1], Or, Lr, tag=f"config5 b{b} h{h}")
+
+
+@pytest.mark.parametrize("D,Hkv,dtype", [(64, 4, torch.float16), (128, 4, torch.float16),
+                                         (64, 1, torch.float16), (128, 2, torch.float16),
+                                         (128, 4, torch.bfloat16)])
+def test_garbage_past_context_is_ignored(fa, dev, D, Hkv, dtype):
+    """Slots past ctx in a sequence's last page hold whatever the pool held
+    (pools come from torch.empty; kv_append writes only up to the context).
+    NaN and Inf there must not reach O or L: the result equals the oracle's,
+    which gathers only the first ctx tokens, for the one-head-per-workgroup
+    kernel (Hkv = H) and the grouped kernels (Hkv < H)."""
+    H = 4
+    ctx = [1, 15, 17, 40, 300, 33]
+    q, kp, vp, table, ctxa = _small(21 + D + Hkv, B=len(ctx), H=Hkv, D=D, ctx=ctx, extra_pages=1)
+    q = np.random.default_rng(22).standard_normal((len(ctx), H, D)).astype(np.float16)
+    if dtype == torch.bfloat16:   # values exactly representable in both formats
+        q = (np.round(q.astype(np.float32) * 8) / 8).astype(np.float16)
+        kp = (np.round(kp.astype(np.float32) * 8) / 8).astype(np.float16)
+        vp = (np.round(vp.astype(np.float32) * 8) / 8).astype(np.float16)
+    kg, vg = kp.copy(), vp.copy()
+    for b, n in enumerate(ctx):
+        last = table[b, (n - 1) // 16]
+        if n % 16:
+            kg[last, :, n % 16:, ::2] = np.inf
+            kg[last, :, n % 16:, 1::2] = np.nan
+            vg[last, :, n % 16:, ::3] = np.nan
+            vg[last, :, n % 16:, 1::3] = np.inf
+            vg[last, :, n % 16:, 2::3] = -np.inf
+    tq, tk, tv, tt, tc = _dev(dev, q, kg, vg, table, ctxa)
+    tq, tk, tv = tq.to(dtype), tk.to(dtype), tv.to(dtype)
+    g = H // Hkv
+    Or, Lr = decode_attention(q, np.repeat(kp, g, axis=1), np.repeat(vp, g, axis=1), table, ctxa)
+    for S in (1, 3):
+        O, L = fa.decode_paged(tq, tk, tv, tt, tc, num_splits=S)
+        assert torch.isfinite(O.float()).all() and torch.isfinite(L).all(), f"S{S}: non-finite"
+        Of, Lf = O.float().cpu().numpy(), L.cpu().numpy()
+        tol = 2e-3 if dtype == torch.float16 else 1e-2
+        assert np.abs(Of - Or).max() <= tol, f"S{S} O {np.abs(Of - Or).max():.3e}"
+        assert (np.abs(Lf - Lr) / np.maximum(np.abs(Lr), 1.0)).max() <= 1e-4
