@@ -37,15 +37,9 @@ METRIC = "FA fwd TFLOP/s & % FP16 MFMA peak at B1 H8 N4096 D64; decode GB/s"
 def kernel_name(variant, D, causal=False, write_l=True, full=True):
     """Template instance of the forward kernel behind a variant code."""
     c, w, f = (str(x).lower() for x in (causal, write_l, full))
-    if variant == 204:
-        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4,false,2,1>"
-    if variant == 308:
-        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},8,false,4,1>"
-    if variant == 404:
-        return f"fa_fwd_pp_kernel<{D},{c},{w},{f},4,false,2,2>"
-    if variant > 100:
-        return f"fa_fwd_pipe_kernel<{D},{c},{w},{f},{variant % 10},{(variant - 100) // 10}>"
-    return f"fa_fwd_split_kernel<{D},{c},{w},{f},{variant // 10},{variant % 10}>"
+    if variant in (506, 508):
+        return f"fa_fwd_rp_kernel<{c},{w},{f},{variant - 500}>"
+    return f"fa_fwd_pp_kernel<{D},{c},{w},{f},{variant - 200}>"
 
 
 def pmc_traffic(kernel):
@@ -87,6 +81,44 @@ def time_events(fn, warmup, iters, torch):
 
 def median_of(fn, reps, warmup, iters, torch):
     return statistics.median(time_events(fn, warmup, iters, torch) for _ in range(reps))
+
+
+def burn_in(fn, seconds, torch, depth=256):
+    """Back-to-back calls of fn for `seconds` of wall time, so the clocks have
+    settled at their loaded level when the caller's next calls start. At most
+    `depth` calls are queued ahead of the GPU (an event every `depth` calls is
+    waited for), and the queue is left running: no synchronisation at the end."""
+    marks = []
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while time.perf_counter() < t_end:
+        fn()
+        n += 1
+        if n % depth == 0:
+            e = torch.cuda.Event()
+            e.record()
+            marks.append(e)
+            if len(marks) > 1:
+                marks.pop(0).synchronize()
+    return n
+
+
+def paired_delta(fn_a, fn_b, reps, iters, torch):
+    """Median per-rep times of fn_a and fn_b and the median of the per-rep
+    differences b - a, with the two run back to back in alternating order
+    (the reference's protocol, bench/bench_fa3_headline.py:73-81)."""
+    ta, tb, d = [], [], []
+    for r in range(reps):
+        if r % 2 == 0:
+            a = time_events(fn_a, 5, iters, torch)
+            b = time_events(fn_b, 5, iters, torch)
+        else:
+            b = time_events(fn_b, 5, iters, torch)
+            a = time_events(fn_a, 5, iters, torch)
+        ta.append(a)
+        tb.append(b)
+        d.append(b - a)
+    return statistics.median(ta), statistics.median(tb), statistics.median(d)
 
 
 def make_fwd(torch, dev, B, H, N, D, seed, amp=1.0):
@@ -239,10 +271,7 @@ def bench_sdpa(fa, torch, dev, reps=10):
         return res
     be = getattr(SDPBackend, res["sdpa_backend"])
 
-    def med(xs):
-        xs = sorted(xs)
-        n = len(xs)
-        return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+    med = statistics.median
 
     for N in (1024, 2048, 4096):
         g = torch.Generator(device=dev).manual_seed(N)
@@ -387,6 +416,8 @@ def main():
                                        "copy"],
                     default="all")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--burn-in", type=float, default=1.5,
+                    help="seconds of back-to-back headline calls before the warmup steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -422,12 +453,12 @@ def main():
 
     B, H, N, D = 1, 8, 4096, 64
     Q, K, V = make_fwd(torch, dev, B, H, N, D, seed=42)
-    # burn-in (the reference's clock warm-up, bench/bench_fa3_headline.py:53-56)
-    for _ in range(100):
-        fa.forward_only(Q, K, V)
-    torch.cuda.synchronize()
-
     step = lambda: fa.forward(Q, K, V)  # noqa: E731
+    # Burn-in (the reference's clock warm-up, bench/bench_fa3_headline.py:53-56),
+    # time-based: a few hundred calls do not reach the loaded clock, and a
+    # 20-step window right after them caught the ramp. The burn-in runs
+    # straight into the warmup steps; one synchronisation opens the window.
+    burn_calls = burn_in(step, args.burn_in, torch)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -457,6 +488,7 @@ def main():
                    "B": B, "H": H, "N": N, "D": D, "causal": False},
         "pct_fp16_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 2),
         "wall_s_timed_region": round(wall_s, 4),
+        "burn_in": {"seconds": args.burn_in, "calls": burn_calls},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": pmc_traffic(kname),
@@ -468,9 +500,14 @@ def main():
 
     if args.only == "all":
         extra = {}
-        oo = median_of(lambda: fa.forward_only(Q, K, V), 5, 10, 100, torch)
-        wl = median_of(step, 5, 10, 100, torch)
-        extra["N4096_O+L_vs_O-only_ms"] = [round(wl, 5), round(oo, 5)]
+        # steady state of the same step (the headline window's check), and
+        # O+L against O-only in alternating pairs
+        burn_in(step, 0.5, torch)
+        wl, oo, delta = paired_delta(step, lambda: fa.forward_only(Q, K, V), 11, 100, torch)
+        extra["N4096_steady_state_ms"] = round(median_of(step, 5, 10, 200, torch), 5)
+        extra["N4096_O+L_vs_O-only"] = {"O+L_ms": round(wl, 5), "O-only_ms": round(oo, 5),
+                                        "paired_median_delta_us": round(delta * 1000, 3),
+                                        "reps": 11, "calls_per_rep": 100}
         split_plan = fa.probe.probe_fwd_splitkv_plan
         for n in (1024, 2048, 8192):
             q, k, v = make_fwd(torch, dev, 1, 8, n, 64, seed=n)
