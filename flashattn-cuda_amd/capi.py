@@ -57,7 +57,7 @@ SIGNATURES = {
     "fa_bwd_varlen_f16": (C.c_int, [_vp] * 11 + [_i64] * 6 + [C.c_int, _vp]),
     "fa_validate_bwd_varlen": (C.c_int, [_vp] * 11 + [_i64] * 6),
     "fa_probe_fwd_variant": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp]),
-    "fa_probe_fwd_variants": (C.c_int, [_vp, C.c_int, _i64]),
+    "fa_probe_fwd_variants": (C.c_int, [_vp, C.c_int, _i64, C.c_int]),
     "fa_probe_default_variant": (C.c_int, [_i64]),
 }
 

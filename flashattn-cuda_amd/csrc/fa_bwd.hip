@@ -626,22 +626,14 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const int nb = (geo.N + kBlk - 1) / kBlk;
   const int total = (int)(units * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
-  // FA_MI355X_BWD_FUSED=0 (read once) launches the two kernels separately,
-  // for measurement.
-  static const bool fused = [] {
-    const char* e = getenv("FA_MI355X_BWD_FUSED");
-    return !(e && e[0] == '0');
-  }();
   bool launched = false;
   // One launch where it pays (measured): at D = 64 always, at D = 128 for
   // causal heads (B1 H8 N4096: 0.255 -> 0.186 ms), not for non-causal ones
   // (B4 H16 N4096: 2.36 -> 2.50 ms), whose units are all the same length.
   if constexpr (GK == 2 && GQ == 2 && (D == 64 || CAUSAL)) {
-    if (fused) {
-      hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
-                         s, Q, K, V, G, nl, di, dk_q, dv_q, dq, geo, nb, total, c, scale);
-      launched = true;
-    }
+    hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
+                       s, Q, K, V, G, nl, di, dk_q, dv_q, dq, geo, nb, total, c, scale);
+    launched = true;
   }
   if (!launched) {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,

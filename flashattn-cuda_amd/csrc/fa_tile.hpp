@@ -82,6 +82,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
+// make_rsrc for a wave-uniform range that must sit in SGPRs (the inline
+// asm of the LDS copies below takes the descriptor as an SGPR operand): the
+// base and length go through readfirstlane, which is free when the compiler
+// already holds them in SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_s(const void* base, int bytes) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const void* p = reinterpret_cast<const void*>(((uintptr_t)hi << 32) | lo);
+  return make_rsrc(p, __builtin_amdgcn_readfirstlane(bytes));
+}
+
 // LDS byte address of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;

@@ -280,7 +280,7 @@ std::vector<torch::Tensor> backward_varlen(torch::Tensor q, torch::Tensor k, tor
 // Test support: the forward through one explicit kernel variant.
 std::vector<torch::Tensor> probe_fwd_variant(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                                              bool causal, int64_t variant, bool want_L) {
-  TORCH_CHECK(variant > 0, "variant must be > 0");
+  TORCH_CHECK(variant > 0, "variant must be > 0 (1000 + v: v's guarded instance)");
   auto r = forward_impl(Q, K, V, want_L, causal, (int)variant);
   if (want_L) return {r.first, r.second};
   return {r.first};
@@ -291,15 +291,16 @@ std::vector<torch::Tensor> probe_fwd_variant(torch::Tensor Q, torch::Tensor K, t
 std::vector<torch::Tensor> probe_fwd_splitkv(torch::Tensor Q, torch::Tensor K, torch::Tensor V,
                                              bool causal, int64_t splits, bool want_L) {
   TORCH_CHECK(splits >= 1 && splits <= 16, "splits must be in [1, 16]");
-  auto r = splits == 1 ? forward_impl(Q, K, V, want_L, causal, /*variant=*/204)
+  const int def = fa_probe_default_variant(Q.size(3));
+  auto r = splits == 1 ? forward_impl(Q, K, V, want_L, causal, def)
                        : forward_impl(Q, K, V, want_L, causal, 0, splits);
   if (want_L) return {r.first, r.second};
   return {r.first};
 }
 
-std::vector<int64_t> probe_fwd_variants(int64_t D) {
+std::vector<int64_t> probe_fwd_variants(int64_t D, bool causal) {
   int buf[64];
-  const int n = fa_probe_fwd_variants(buf, 64, D);
+  const int n = fa_probe_fwd_variants(buf, 64, D, causal ? 1 : 0);
   return std::vector<int64_t>(buf, buf + (n < 64 ? n : 64));
 }
 

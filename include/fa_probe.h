@@ -44,20 +44,23 @@ int fa_probe_chain(const void* q, const void* k, const void* v, float* o, int64_
                    void* stream);
 
 /* fa_fwd_f16 with an explicit kernel variant (the codes fa_probe_fwd_variants
- * lists for D), so the tests can check every variant in one process. Returns
- * FA_ERR_HEAD_DIM for a variant that does not exist for D. */
+ * lists for D, or 0 for the default), so the tests can check every variant in
+ * one process. 1000 + v runs variant v through its guarded instance (bounds
+ * predicates compiled in) even where N is a multiple of the 128-row block, for
+ * the full-tile vs guarded identity. Returns FA_ERR_HEAD_DIM for a variant
+ * that does not exist for D. */
 int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o, float* lse,
                          int64_t B, int64_t H, int64_t N, int64_t D, int causal, int variant,
                          void* stream);
 
-/* The variant fa_fwd_f16 runs for head dimension D (0 for another D):
- * 10*k + s = split kernel (k key slices, s LDS stages), 100 + 10*r + k =
- * pipelined kernel (k key slices, ring of r slots), 204 = ping-pong kernel. */
+/* The variant fa_fwd_f16 runs for head dimension D, non-causal (0 for another D):
+ * 204 = ping-pong kernel (32 rows per wave, ring of 4 tiles), 506 / 508 =
+ * row-pair kernel (D = 64, 64 rows per wave, ring of 6 / 8 tiles). */
 int fa_probe_default_variant(int64_t D);
 
-/* Writes up to max_out variant codes that exist for head dimension D into out
- * (may be NULL) and returns how many there are. */
-int fa_probe_fwd_variants(int* out, int max_out, int64_t D);
+/* Writes up to max_out variant codes that exist for head dimension D and the
+ * causal flag into out (may be NULL) and returns how many there are. */
+int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal);
 
 #ifdef __cplusplus
 }
