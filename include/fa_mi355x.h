@@ -242,9 +242,10 @@ int64_t fa_decode_workspace_floats(int64_t B, int64_t H, int64_t D,
  * normalised partial attention of q[b,h] over the split's pages.
  * Sequence b has ceil(ctx_lens[b]/page_size) pages, divided into num_splits
  * runs of ceil(pages/num_splits) pages. An empty split writes part_o = 0 and
- * part_lse = -inf. A page id outside [0, num_pages) or ctx_lens[b] beyond
- * max_pages*page_size makes every partial of that sequence NaN (no memory
- * outside the pool is read). No reference counterpart.
+ * part_lse = -inf. A page id outside [0, num_pages) makes the partials of
+ * the splits that touch the bad page NaN; a negative ctx_lens[b] or one
+ * beyond max_pages*page_size makes every partial of that sequence NaN. No
+ * memory outside the pool is read. No reference counterpart.
  */
 int fa_decode_split_f16(const void* q, const void* k_pool, const void* v_pool,
                         const int32_t* page_table, const int32_t* ctx_lens,
@@ -255,7 +256,8 @@ int fa_decode_split_f16(const void* q, const void* k_pool, const void* v_pool,
 /*
  * Combine pass: L = log sum_s exp(part_lse_s); o = sum_s exp(part_lse_s - L)
  * part_o_s, written as fp16 o [B, H, D] and fp32 lse [B, H] (lse may be NULL).
- * If every split is empty, o = 0 and lse = -inf. No reference counterpart.
+ * If every split is empty, o = 0 and lse = -inf; a NaN partial makes o and
+ * lse of its (b, h) NaN. No reference counterpart.
  */
 int fa_lse_combine_f32(const float* part_o, const float* part_lse,
                        int64_t B, int64_t H, int64_t D, int64_t num_splits,
