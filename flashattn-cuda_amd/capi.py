@@ -45,6 +45,7 @@ SIGNATURES = {
     "fa_fwd_varlen_f16": (C.c_int, [_vp] * 6 + [_i64] * 6 + [C.c_int, _vp]),
     "fa_decode_paged_gqa_f16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 5),
     "fa_decode_paged_bf16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 5),
+    "fa_decode_paged_noalloc_f16": (C.c_int, [_vp] * 5 + [_i64] * 8 + [_vp] * 3),
     "fa_validate_kv_append": (C.c_int, [_vp] * 8 + [_i64] * 7),
     "fa_kv_append_f16": (C.c_int, [_vp] * 8 + [_i64] * 7 + [_vp]),
     "fa_kv_append_bf16": (C.c_int, [_vp] * 8 + [_i64] * 7 + [_vp]),
@@ -61,11 +62,13 @@ SIGNATURES = {
     "fa_probe_default_variant": (C.c_int, [_i64]),
 }
 
+DECODE_SCRATCH_FLOATS = 1 << 22   # FA_DECODE_SCRATCH_FLOATS
+
 STATUS = {
     "FA_OK": 0, "FA_ERR_NULL_POINTER": 1, "FA_ERR_HEAD_DIM": 2, "FA_ERR_SEQ_LEN": 3,
     "FA_ERR_BATCH_HEADS": 4, "FA_ERR_ALIGNMENT": 5, "FA_ERR_TOO_LARGE": 6,
     "FA_ERR_PAGE_SIZE": 7, "FA_ERR_NUM_SPLITS": 8, "FA_ERR_MAX_PAGES": 9,
-    "FA_ERR_NUM_PAGES": 10, "FA_ERR_KV_HEADS": 11,
+    "FA_ERR_NUM_PAGES": 10, "FA_ERR_KV_HEADS": 11, "FA_ERR_SCRATCH_SIZE": 12,
 }
 
 

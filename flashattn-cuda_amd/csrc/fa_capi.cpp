@@ -34,6 +34,8 @@ extern "C" const char* fa_status_str(int status) {
     case FA_ERR_MAX_PAGES: return "max_pages must be > 0";
     case FA_ERR_NUM_PAGES: return "num_pages must be > 0";
     case FA_ERR_KV_HEADS: return "H must be a positive multiple of H_kv";
+    case FA_ERR_SCRATCH_SIZE:
+      return "B*H*num_splits*(D+1) exceeds FA_DECODE_SCRATCH_FLOATS (no-alloc decode)";
     default: break;
   }
   if (status < 0) return "HIP error (negated hipError_t)";

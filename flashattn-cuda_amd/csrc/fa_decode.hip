@@ -19,6 +19,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "fa_mi355x.h"
 #include "fa_tile.hpp"
 
@@ -571,4 +573,71 @@ extern "C" int fa_decode_paged_bf16(const void* q, const void* k_pool, const voi
   return fa::decode_paged_gqa<true>(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D,
                                     page_size, max_pages, num_pages, num_splits, part_o,
                                     part_lse, o, lse, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free paged decode: the split partials (part_o, then part_lse)
+// live in a file-scope device array instead of a caller workspace, for
+// callers that cannot allocate device memory. The split pass writes every
+// partial it owns (an empty split writes 0 and -inf), so nothing in the array
+// needs clearing between calls.
+namespace fa {
+// One copy per GPU that loads this library, held until the process ends. In
+// host code `scratch` names a host-side stand-in: only the address returned
+// by hipGetSymbolAddress for the current device may reach a kernel.
+static __device__ __align__(256) float scratch[FA_DECODE_SCRATCH_FLOATS];
+
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_addr[kScratchDevices];   // per device, null until resolved
+
+// Device address of `scratch` on device `dev`, resolved on first use with
+// `dev` current (then the previous current device is restored).
+static int scratch_addr(int dev, float** out) {
+  if (dev < 0 || dev >= kScratchDevices) return -(int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return -(int)e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return -(int)e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t e2 = cur != dev ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return -(int)e;
+    if (e2 != hipSuccess) return -(int)e2;
+    if (p == nullptr) return -(int)hipErrorInvalidSymbol;
+    g_scratch_addr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_addr[dev];
+  return FA_OK;
+}
+}  // namespace fa
+
+extern "C" int fa_decode_paged_noalloc_f16(const void* q, const void* k_pool,
+                                           const void* v_pool, const int32_t* page_table,
+                                           const int32_t* ctx_lens, int64_t B, int64_t H,
+                                           int64_t H_kv, int64_t D, int64_t page_size,
+                                           int64_t max_pages, int64_t num_pages,
+                                           int64_t num_splits, void* o, float* lse,
+                                           void* stream) {
+  int st = fa_validate_decode(q, k_pool, v_pool, page_table, ctx_lens, B, H, D, page_size,
+                              max_pages, num_pages, num_splits);
+  if (st != FA_OK) return st;
+  if (o == nullptr) return FA_ERR_NULL_POINTER;
+  if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
+  // B, H, D and num_splits are bounded by the validation above, so the
+  // product cannot overflow.
+  if (B * H * num_splits * (D + 1) > FA_DECODE_SCRATCH_FLOATS) return FA_ERR_SCRATCH_SIZE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int dev = 0;
+  hipError_t e = s != nullptr ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return -(int)e;
+  float* part_o = nullptr;
+  st = fa::scratch_addr(dev, &part_o);
+  if (st != FA_OK) return st;
+  float* part_lse = part_o + B * H * num_splits * D;
+  return fa::decode_paged_gqa<false>(q, k_pool, v_pool, page_table, ctx_lens, B, H, H_kv, D,
+                                     page_size, max_pages, num_pages, num_splits, part_o,
+                                     part_lse, o, lse, stream);
 }

@@ -44,8 +44,13 @@ enum fa_status_code {
   FA_ERR_NUM_SPLITS = 8,     /* num_splits outside [1, 16] */
   FA_ERR_MAX_PAGES = 9,      /* max_pages <= 0 */
   FA_ERR_NUM_PAGES = 10,     /* num_pages <= 0 */
-  FA_ERR_KV_HEADS = 11       /* H_kv <= 0 or H not a multiple of H_kv */
+  FA_ERR_KV_HEADS = 11,      /* H_kv <= 0 or H not a multiple of H_kv */
+  FA_ERR_SCRATCH_SIZE = 12   /* split partials exceed FA_DECODE_SCRATCH_FLOATS */
 };
+
+/* Floats of the library's own split-partials array used by
+ * fa_decode_paged_noalloc_f16 (16 MiB per GPU). */
+#define FA_DECODE_SCRATCH_FLOATS (((int64_t)1) << 22)
 
 /* Human-readable name of a status code (static storage). */
 const char* fa_status_str(int status);
@@ -282,6 +287,28 @@ int fa_decode_paged_gqa_f16(const void* q, const void* k_pool, const void* v_poo
                             int64_t H, int64_t H_kv, int64_t D, int64_t page_size,
                             int64_t max_pages, int64_t num_pages, int64_t num_splits,
                             float* part_o, float* part_lse, void* o, float* lse, void* stream);
+
+/*
+ * fa_decode_paged_gqa_f16 that allocates nothing and takes no workspace: the
+ * split partials go to a static device array of FA_DECODE_SCRATCH_FLOATS
+ * floats that the library holds on each GPU it runs on until the process
+ * ends (its address is resolved once per device, on that device's first
+ * call). Needs B*H*num_splits*(D+1) <= FA_DECODE_SCRATCH_FLOATS, else
+ * FA_ERR_SCRATCH_SIZE (B = 32, H = 32, D = 128, 16 splits uses half). Makes
+ * no hipMalloc/hipFree or other allocating call. Nothing in the array has to
+ * start at zero (every partial a call reads, that call wrote). All calls on
+ * one GPU share the array, so calls that overlap on one GPU (different
+ * streams, or host threads) race; calls on one stream are ordered. Same
+ * arguments, layouts and results as fa_decode_paged_gqa_f16, bit for bit.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).
+ */
+int fa_decode_paged_noalloc_f16(const void* q, const void* k_pool, const void* v_pool,
+                                const int32_t* page_table, const int32_t* ctx_lens, int64_t B,
+                                int64_t H, int64_t H_kv, int64_t D, int64_t page_size,
+                                int64_t max_pages, int64_t num_pages, int64_t num_splits,
+                                void* o, float* lse, void* stream);
 
 /*
  * fa_decode_paged_gqa_f16 for bf16 q, pools and O (same layouts and

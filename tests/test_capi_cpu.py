@@ -83,6 +83,22 @@ def test_validate_decode(capi, kw, code):
     assert lib.fa_validate_decode(*_dec(**kw)) == capi.STATUS[code]
 
 
+def test_noalloc_decode_rejects_before_touching_the_device(capi):
+    lib = capi.load()
+    fn = lib.fa_decode_paged_noalloc_f16
+    head = (A, A, A, A, A)
+    # 64 * 32 * 16 * (128 + 1) floats of partials exceed the 2^22 of the array
+    assert 64 * 32 * 16 * 129 > capi.DECODE_SCRATCH_FLOATS
+    assert fn(*head, 64, 32, 32, 128, 16, 2048, 33000, 16, A, A, None) == \
+        capi.STATUS["FA_ERR_SCRATCH_SIZE"]
+    assert fn(*head, 32, 32, 5, 128, 16, 2048, 33000, 16, A, A, None) == \
+        capi.STATUS["FA_ERR_KV_HEADS"]
+    assert fn(*head, 32, 32, 8, 128, 16, 2048, 33000, 16, None, A, None) == \
+        capi.STATUS["FA_ERR_NULL_POINTER"]
+    assert fn(*head, 32, 32, 8, 128, 16, 2048, 33000, 17, A, A, None) == \
+        capi.STATUS["FA_ERR_NUM_SPLITS"]
+
+
 def test_decode_rejects_before_touching_the_device(capi):
     lib = capi.load()
     args = _dec(S=20)
