@@ -37,8 +37,6 @@ METRIC = "FA fwd TFLOP/s & % FP16 MFMA peak at B1 H8 N4096 D64; decode GB/s"
 def kernel_name(variant, D, causal=False, write_l=True, full=True):
     """Template instance of the forward kernel behind a variant code."""
     c, w, f = (str(x).lower() for x in (causal, write_l, full))
-    if variant in (506, 508):
-        return f"fa_fwd_rp_kernel<{c},{w},{f},{variant - 500}>"
     return f"fa_fwd_pp_kernel<{D},{c},{w},{f},{variant - 200}>"
 
 

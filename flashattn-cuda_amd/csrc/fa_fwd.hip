@@ -19,14 +19,10 @@
 //     running max m; the lane's tile sum bounds every P it holds, and only when
 //     it exceeds 2^15 (first tile, or a much larger new maximum) is m raised
 //     and O rescaled. P <= 2^15 stays inside fp16 and the fp32 accumulators.
-// Two kernels share that per-wave core (RowBlock, 32 rows):
-//   * fa_fwd_pp_kernel: two wave groups own the even and odd key tiles of the
-//     same rows and alternate, barrier by barrier, between a matrix phase and
-//     a softmax phase, so each SIMD runs one wave's MFMAs while the other
-//     wave's VALU work issues;
-//   * fa_fwd_rp_kernel (D = 64): the same alternation with 64 rows per wave
-//     (two RowBlocks) and four key-tile groups, so every K/V fragment read
-//     from LDS feeds two MFMAs.
+// The kernel, fa_fwd_pp_kernel, is built on a per-wave core (RowBlock, 32
+// rows): two wave groups own the even and odd key tiles of the same rows and
+// alternate, barrier by barrier, between a matrix phase and a softmax phase,
+// so each SIMD runs one wave's MFMAs while the other wave's VALU work issues.
 // Template flags: D in {64,128}, CAUSAL, WRITE_L (O-only when false), FULL
 // (N % 128 == 0: no bounds predicates).
 #include <hip/hip_runtime.h>
@@ -196,17 +192,6 @@ struct RowBlock {
     return expo_pack<NB>(s, pf, m_safe());
   }
 
-  // O^T += V^T P^T over the PV k-steps of the blocks.
-  template <int NB>
-  __device__ __forceinline__ void pv(const char* vs, int kb0, const f16x8 (&pf)[2 * NB]) {
-#pragma unroll
-    for (int j = 0; j < 2 * NB; ++j) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        o[db] = mma32<BF16>(load_v_frag<D>(vs, 2 * kb0 + j, db, lane), pf[j], o[db]);
-    }
-  }
-
   // Merge another wave's (m, l, O) for the same rows, read from LDS.
   __device__ __forceinline__ void merge_from(const float* src) {
     const float m2 = src[lane];
@@ -301,16 +286,44 @@ struct RowBlock {
   }
 };
 
-// Per-lane DMA source offsets of 1 KiB block b of a tile: lane l writes bytes
-// [16 l, 16 l + 16) of the block, so the XOR swizzle of the LDS layout is
-// applied by choosing which global chunk the lane fetches.
+// LDS layouts of a 64-key tile, copied as 1 KiB blocks (lane l of a copy
+// writes bytes [16 l, 16 l + 16) of its block, so a layout is chosen by which
+// global 16-byte chunk each lane fetches):
+//   * K: row-major [key][D] with the XOR swizzle of k_off;
+//   * V: one block per PV operand fragment. Block b = ks * (D / 32) + db
+//     holds keys 16 ks .. 16 ks + 15 as 64-byte rows of columns 32 db ..
+//     32 db + 31, so the PV k-steps, in the order the matrix phases issue them
+//     (k-step outer, d-block inner), read their fragments at increasing
+//     addresses. With the row-major layout the d-blocks of one k-step share
+//     rows and the reads alternate between them, which made the transposed
+//     reads of a matrix phase ~12% slower (measured on MI355X). The
+//     transposed reads of a block are conflict-free without a swizzle: the
+//     32 lanes of a half wave cover 4 rows x 64 bytes, i.e. each of the 64
+//     banks once.
 template <int D>
 __device__ __forceinline__ void dma_offsets(int b, int lane, uint32_t& koff, uint32_t& voff) {
   const int o = b * 1024 + 16 * lane;
   const int r = o / (2 * D);
   const int slot = (o % (2 * D)) / 16;
   koff = (uint32_t)(r * 2 * D + (slot ^ k_swz<D>(r)) * 16);
-  voff = (uint32_t)(r * 2 * D + (slot ^ v_swz<D>(r)) * 16);
+  constexpr int DB = D / 32;
+  const int ks = b / DB, db = b % DB;
+  voff = (uint32_t)((16 * ks + (lane >> 2)) * 2 * D + (4 * db + (lane & 3)) * 16);
+}
+
+// Lane offset, within a V block, of the transposed read of the block's lower
+// 8 keys (the upper 8 follow at +512): lane l gets column 32 db + l % 32 of
+// keys 4 (l / 32) .. + 3, the P^T key order of the S^T accumulators.
+__device__ __forceinline__ int vblk_lane_off(int lane) {
+  const int s = lane & 15;
+  return (4 * (lane >> 5) + (s >> 2)) * 64 + 32 * ((lane >> 4) & 1) + 8 * (s & 3);
+}
+
+// The A operand (V^T) of PV fragment b, p = block b + vblk_lane_off(lane).
+__device__ __forceinline__ f16x8 vblk_frag(lds_cp p) {
+  const f16x4 lo = lds_tr16(p);
+  const f16x4 up = lds_tr16(p + 512);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
 }
 
 // Copy one 1 KiB block of tile t of a head (K or V) into dst. The buffer
@@ -327,423 +340,6 @@ __device__ __forceinline__ void dma_block_or_zero(const char* head, int head_byt
   dma16(make_rsrc_s(head + done, bytes), dst, off);
 }
 
-
-// ---------------------------------------------------------------------------
-// Row-pair ping-pong kernel (D = 64): 8 waves over the workgroup's 128 query
-// rows, every wave owning 64 of them (two 32-row blocks), and four key-tile
-// groups. Wave w runs on SIMD w % 4: rows 64 (w & 1) .., parity (w >> 1) & 1,
-// team w >> 2; its group g = parity + 2 team owns the key tiles t = g (mod 4).
-// The two waves of a SIMD (one per team) hold the same rows and alternate,
-// barrier by barrier, between a matrix phase and a softmax phase, as in
-// fa_fwd_pp_kernel. Each K or V fragment a wave reads from LDS feeds two
-// MFMAs (one per row block), half the LDS operand reads per MFMA of a 32-row
-// wave.
-//
-//   phase      2j                          2j+1
-//   team 0     S(step j)                   M(PV step j, QK step j+1)
-//   team 1     M(PV step j-1, QK step j)   S(step j)
-//
-// Step j of group g is tile 4j + g, so phase p's M waves read K tiles 2p+2,
-// 2p+3 and V tiles 2p-2, 2p-1. K and V tiles go through rings of RING slots
-// (tile x in slot x % RING). In phase p the four M waves copy, one tile
-// each, K tiles 2p+2A+2, 2p+2A+3 and V tiles 2p+2A-2, 2p+2A-1, A = RING/2-1
-// phases ahead of their reads; each overwrites a tile read in phase p-1. A
-// wave waits for its copies at the end of its next (softmax) phase. Copies
-// past the last tile use an empty buffer range (zeros, no memory read).
-//
-// Q goes HBM -> LDS once per workgroup and each wave reads its Q^T operands
-// from there into registers.
-//
-// At the end, the four waves of a row half (groups 0..3, the same 64 rows)
-// exchange their partial (m, l, O) through LDS and each merges one 32 x 32
-// block of O; the blocks are staged in LDS and stored as whole rows.
-// ---------------------------------------------------------------------------
-template <bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false>
-__global__ void __launch_bounds__(512)
-fa_fwd_rp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
-                 const f16* __restrict__ V, f16* __restrict__ O,
-                 float* __restrict__ L, Geom geo, int num_qb, int total, float c) {
-  constexpr int D = 64;
-  constexpr int TILE = kBC * D * 2;              // 8 KiB
-  constexpr int BLOCKS = TILE / 1024;            // 1 KiB copies per tile
-  constexpr int A = RING / 2 - 1;                // copy lead, in phases
-  static_assert(RING == 6 || RING == 8, "ring of 6 or 8 tiles");
-  using RB = RowBlock<D, CAUSAL, FULL, BF16>;
-  // Epilogue LDS: per row half, (m, l) of the 4 waves x 2 row blocks, O blocks
-  // sent to the 3 other waves (16 floats per lane each), and a 64-row stage.
-  constexpr int ML_FLOATS = 4 * 2 * 2 * 64;
-  constexpr int OX_FLOATS = 4 * 3 * 16 * 64;
-  constexpr int STAGE_STRIDE = 2 * D + 16;       // padded row: spreads the LDS banks
-  constexpr int HALF_BYTES = (ML_FLOATS + OX_FLOATS) * 4 + 64 * STAGE_STRIDE;
-  constexpr int RING_BYTES = 2 * RING * TILE;
-  constexpr int Q_BYTES = 2 * TILE;              // the workgroup's 128 Q rows
-  constexpr int SMEM = RING_BYTES + Q_BYTES > 2 * HALF_BYTES ? RING_BYTES + Q_BYTES : 2 * HALF_BYTES;
-  static_assert(SMEM <= 160 * 1024, "LDS");
-  constexpr int PF = 4;                          // operand prefetch distance, in fragments
-  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rh = wave & 1;                        // row half
-  const int par = (wave >> 1) & 1;
-  const int team = wave >> 2;
-  const int g = par + 2 * team;                   // tile group
-  const int cslot = 2 * par + rh;                 // which tile of a phase this wave copies
-
-  const int logical = xcd_remap(blockIdx.x, total);
-  const int bh = logical / num_qb;
-  int qb = logical - bh * num_qb;
-  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
-
-  const HeadView hv = head_view<D>(geo, bh);
-  const int N = hv.n;
-  if (qb * kBR >= N) return;   // varlen: past this sequence (whole workgroup)
-  const size_t head = hv.q;
-  const int head_bytes = N * D * 2;
-  const int q0 = qb * kBR;
-
-  RB rb[2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) rb[r].setup(lane, q0 + 64 * rh + 32 * r, N, c);
-
-  const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
-  const int n_tiles = (kv_end + kBC - 1) / kBC;
-  const int n_steps = (n_tiles + 3) / 4;
-  const char* Kh = reinterpret_cast<const char*>(K + hv.kv);
-  const char* Vh = reinterpret_cast<const char*>(V + hv.kv);
-  const uint32_t lds0 = lds_addr(smem);
-
-  // Per-lane source offsets within a 1 KiB block: they depend on the block
-  // only through its parity (K layout) or not at all (V).
-  uint32_t koff[2], voff;
-  {
-    uint32_t k0, v0, k1, v1;
-    dma_offsets<D>(0, lane, k0, v0);
-    dma_offsets<D>(1, lane, k1, v1);
-    koff[0] = k0;
-    koff[1] = k1 - 1024;
-    voff = v0;
-  }
-  // Block b of K (is_v false) or V tile x into its ring slot; past the last
-  // tile (or past N) the range is empty and the copy writes zeros.
-  auto copy_block = [&](bool is_v, int x, int b) {
-    const int done = x * TILE + b * 1024;
-    const int live = x < n_tiles ? (FULL ? 1024 : min(1024, head_bytes - done)) : 0;
-    const char* src = (is_v ? Vh : Kh) + (live > 0 ? done : 0);
-    const uint32_t dst = lds0 + ((is_v ? RING : 0) + x % RING) * TILE + b * 1024;
-    dma16(make_rsrc_s(src, live > 0 ? live : 0), dst, is_v ? voff : koff[b & 1]);
-  };
-
-  // Per-lane operand offsets within a tile, for k-step 0 and d-block 0: at
-  // D = 64 the swizzles make k-step kk's K offset koff0 ^ 32 kk and d-block
-  // 1's V offset voff0 ^ 64 (the XOR reaches bits 5 and 6 only; tile bases
-  // and row offsets leave them zero), which saves holding six registers.
-  const uint32_t koff0 = k_frag_off<D>(0, lane);
-  const uint32_t voff0 = v_frag_off<D>(0, lane);
-  auto k_lane = [](uint32_t base0, int kk) { return base0 ^ (uint32_t)(32 * kk); };
-
-  // Prologue, first part: the workgroup's Q rows (two 64-row halves in the K
-  // tile layout, after the ring) and K tiles 0 and 1 (team 0's first QK);
-  // block `wave` of each K tile, Q blocks 2 wave and 2 wave + 1.
-  const uint32_t qarea = lds0 + RING_BYTES;
-  {
-    const char* Qb = reinterpret_cast<const char*>(Q + head);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int qblk = 2 * wave + i;              // of 16
-      const int h = qblk >> 3, b = qblk & 7;
-      const int done = (q0 + 64 * h) * D * 2 + b * 1024;
-      const int live = min(1024, head_bytes - done);
-      dma16(make_rsrc_s(Qb + (live > 0 ? done : 0), live > 0 ? live : 0),
-            qarea + h * TILE + b * 1024, koff[b & 1]);
-    }
-    copy_block(false, 0, wave);
-    copy_block(false, 1, wave);
-  }
-  wait_vmem();
-  __syncthreads();
-  // Q^T operands of this wave's rows; rows past N arrived as zeros.
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      rb[r].qf[kk] = lds_b128(lds_lane_base(k_lane(qarea + rh * TILE + koff0, kk)) + r * 32 * 2 * D);
-  // Prologue, second part: K tiles 2 .. 2A+1 and V tiles 0 .. 2A-3 (those
-  // read before the loop's own copies land), block `wave` of each.
-  constexpr int NK2 = 2 * A, NV2 = 2 * A - 2, PRO2 = NK2 + NV2;
-#pragma unroll
-  for (int x = 0; x < PRO2; ++x) {
-    const bool is_v = x >= NK2;
-    copy_block(is_v, is_v ? x - NK2 : x + 2, wave);
-  }
-
-  f32x16 s[2][2];     // scores of this wave's current tile, [row block][key block]
-  f16x8 p[2][4];      // its packed P, [row block][PV k-step]
-
-  // Matrix phase: PV of tile tv (P in p) and QK of tile tq (into s), the
-  // fragments alternating, each read PF fragments ahead and used by both row
-  // blocks; between them the NC copies of phase ph.
-  auto mphase = [&](auto pv_c, auto qk_c, auto nc_c, int tq, int tv, int ph) {
-    constexpr bool DO_PV = decltype(pv_c)::value;
-    constexpr bool DO_QK = decltype(qk_c)::value;
-    constexpr int NC = decltype(nc_c)::value;
-    constexpr int NF = (DO_PV ? 8 : 0) + (DO_QK ? 8 : 0);
-    uint32_t kt = lds0 + (tq % RING) * TILE;
-    uint32_t vt = lds0 + (RING + tv % RING) * TILE;
-    asm("" : "+s"(kt), "+s"(vt));
-    lds_cp kl[4], vl[2];
-    const uint32_t k0 = kt + koff0, v0 = vt + voff0;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) kl[kk] = lds_lane_base(k_lane(k0, kk));
-    vl[0] = lds_lane_base(v0);
-    vl[1] = lds_lane_base(v0 ^ 64u);
-    // Fragment f: with both, even f = PV fragment f/2, odd f = QK fragment
-    // f/2. PV fragment i: k-step i/2, d-block i%2; QK fragment i: k-step
-    // i/2, key block i%2.
-    auto is_pv = [](int f) { return DO_PV && (!DO_QK || (f & 1) == 0); };
-    auto idx = [](int f) { return (DO_PV && DO_QK) ? f >> 1 : f; };
-    auto fetch = [&](int f) -> f16x8 {
-      const int i = idx(f);
-      if (is_pv(f)) return v_frag_lds<D>(vl[i & 1] + (i >> 1) * 16 * 2 * D);
-      return lds_b128(kl[i >> 1] + (i & 1) * 32 * 2 * D);
-    };
-    const bool cv = cslot >= 2;
-    const int cx = cv ? 2 * ph + 2 * A - 2 + (cslot - 2) : 2 * ph + 2 * A + 2 + cslot;
-    f16x8 op[NF];
-#pragma unroll
-    for (int f = 0; f < PF; ++f) op[f] = fetch(f);
-    __builtin_amdgcn_sched_barrier(0);
-    static_for<0, NF>([&](auto fi) {
-      constexpr int f = decltype(fi)::value;
-      if constexpr (f + PF < NF) op[f + PF] = fetch(f + PF);
-      constexpr int i = idx(f);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        if constexpr (is_pv(f)) {
-          rb[r].o[i & 1] = mma32<BF16>(op[f], p[r][i >> 1], rb[r].o[i & 1]);
-        } else if constexpr (i < 2) {
-          s[r][i & 1] = mma32<BF16>(op[f], rb[r].qf[i >> 1], f32x16{});   // first k-step
-        } else {
-          s[r][i & 1] = mma32<BF16>(op[f], rb[r].qf[i >> 1], s[r][i & 1]);
-        }
-      }
-      static_for<0, NC>([&](auto ci) {
-        constexpr int cc = decltype(ci)::value;
-        if constexpr ((cc + 1) * NF / (NC + 1) == f) copy_block(cv, cx, cc);
-      });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  };
-
-  // Softmax phase of tile t (scores in s) into p; a tile past the end gives
-  // P = 0. The exponentials of a value pair are consumed two pairs later.
-  auto sphase = [&](int t) {
-    if (t >= n_tiles) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[r][j] = f16x8{};
-    } else {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) rb[r].template mask<2>(t, 0, s[r]);
-      const float mc[2] = {rb[0].m_run, rb[1].m_run};
-      constexpr int PAIRS = 32;          // 16 per row block
-      float ex[PAIRS][2];
-      float acc[2][2];
-      static_for<0, PAIRS + 2>([&](auto ui) {
-        constexpr int u = decltype(ui)::value;
-        if constexpr (u < PAIRS) {
-          constexpr int r = u / 16, v = u % 16, b = v / 8, reg = 2 * (v % 8);
-          ex[u][0] = exp2_hw(fmaf(s[r][b][reg], c, -mc[r]));
-          ex[u][1] = exp2_hw(fmaf(s[r][b][reg + 1], c, -mc[r]));
-        }
-        if constexpr (u >= 2) {
-          constexpr int q2 = u - 2, r = q2 / 16, v = q2 % 16;
-          constexpr int b = v / 8, h = (v % 8) / 4, q = v % 4;
-          const f16x2 x = cvt2x<BF16>(ex[q2][0], ex[q2][1]);
-          if constexpr (v < 2) {
-            acc[r][v] = ex[q2][0] + ex[q2][1];
-          } else {
-            acc[r][v & 1] += ex[q2][0] + ex[q2][1];
-          }
-          p[r][2 * b + h][2 * q] = x[0];
-          p[r][2 * b + h][2 * q + 1] = x[1];
-        }
-      });
-      float rs0 = acc[0][0] + acc[0][1];
-      float rs1 = acc[1][0] + acc[1][1];
-      if (__builtin_expect(!__all(rs0 <= kSumLimit && rs1 <= kSumLimit), 0)) {
-        rs0 = rb[0].template rescue<2>(s[0], p[0]);
-        rs1 = rb[1].template rescue<2>(s[1], p[1]);
-      }
-      rb[0].l_run += rs0;
-      rb[1].l_run += rs1;
-    }
-    wait_vmcnt<0>();   // this wave's copies of its previous matrix phase
-  };
-
-  // Keep each phase's register work between its barriers (see
-  // fa_fwd_pp_kernel): the scores are tied to a point after the barrier that
-  // starts the softmax phase and P to a point before the one that ends it.
-  auto pin_s = [&] {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int b = 0; b < 2; ++b) asm volatile("" : "+v"(s[r][b]));
-  };
-  auto pin_p = [&] {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(p[r][j]));
-  };
-  using BT = std::true_type;
-  using BF = std::false_type;
-  using C0 = std::integral_constant<int, 0>;
-  using C8 = std::integral_constant<int, BLOCKS>;
-  auto tile = [&](int j) { return 4 * j + g; };
-
-  if (team == 0) {
-    mphase(BF{}, BT{}, C0{}, tile(0), 0, 0);   // QK of the first tile
-    wait_vmcnt<PRO2 - 2>();                     // K tiles 2, 3 of the prologue (phase 0)
-    __syncthreads();
-    for (int j = 0; j + 1 < n_steps; ++j) {
-      pin_s();
-      sphase(tile(j));                            // phase 2j
-      pin_p();
-      __syncthreads();
-      mphase(BT{}, BT{}, C8{}, tile(j + 1), tile(j), 2 * j + 1);
-      __syncthreads();
-    }
-    pin_s();
-    sphase(tile(n_steps - 1));                    // phase 2n-2
-    pin_p();
-    __syncthreads();
-    mphase(BT{}, BF{}, C0{}, 0, tile(n_steps - 1), 0);   // phase 2n-1: last PV
-    __syncthreads();
-    __syncthreads();                              // phase 2n: team 1's last PV
-  } else {
-    wait_vmcnt<PRO2 - 2>();                       // K tiles 2, 3 of the prologue
-    __syncthreads();
-    mphase(BF{}, BT{}, C8{}, tile(0), 0, 0);      // phase 0: QK only
-    wait_vmcnt<BLOCKS>();   // the rest of the prologue (those of phase 0 stay in flight)
-    __syncthreads();
-    for (int j = 1; j < n_steps; ++j) {
-      pin_s();
-      sphase(tile(j - 1));                        // phase 2j-1
-      pin_p();
-      __syncthreads();
-      mphase(BT{}, BT{}, C8{}, tile(j), tile(j - 1), 2 * j);   // phase 2j
-      __syncthreads();
-    }
-    pin_s();
-    sphase(tile(n_steps - 1));                    // phase 2n-1
-    pin_p();
-    __syncthreads();
-    mphase(BT{}, BF{}, C0{}, 0, tile(n_steps - 1), 0);   // phase 2n: last PV
-    __syncthreads();
-  }
-  wait_vmem();   // every copy has landed before the ring is reused
-  __syncthreads();
-
-  // Merge: wave g of this row half owns O block (row block g / 2, d-block
-  // g % 2). Every wave publishes its (m, l) and sends each other wave that
-  // wave's block of its O; then merges its own block from the four.
-  float* ml = reinterpret_cast<float*>(smem + rh * HALF_BYTES);   // [g][r][m, l][lane]
-  float* ox = ml + ML_FLOATS;                                    // [dst][slot][reg][lane]
-  char* stage = reinterpret_cast<char*>(ox + OX_FLOATS);         // 64 rows
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    ml[((g * 2 + r) * 2 + 0) * 64 + lane] = rb[r].m_run;
-    ml[((g * 2 + r) * 2 + 1) * 64 + lane] = rb[r].l_run;
-  }
-#pragma unroll
-  for (int dst = 0; dst < 4; ++dst) {
-    if (dst == g) continue;
-    const int slot = g < dst ? g : g - 1;
-    const f32x16& blk = rb[dst >> 1].o[dst & 1];
-    float* out = ox + (dst * 3 + slot) * 16 * 64;
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4)
-      *reinterpret_cast<f32x4*>(out + (r4 * 64 + lane) * 4) =
-          f32x4{blk[4 * r4], blk[4 * r4 + 1], blk[4 * r4 + 2], blk[4 * r4 + 3]};
-  }
-  __syncthreads();
-  const int ro = g >> 1, dbo = g & 1;
-  float mw[4], lw[4];
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    mw[w] = ml[((w * 2 + ro) * 2 + 0) * 64 + lane];
-    lw[w] = ml[((w * 2 + ro) * 2 + 1) * 64 + lane];
-    M = fmaxf(M, mw[w]);
-  }
-  float lsum = 0.f, aw[4];
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    aw[w] = (mw[w] == M) ? 1.f : exp2_hw(mw[w] - M);
-    lsum += lw[w] * aw[w];
-  }
-  // g is wave-uniform: pick this wave's block and weight with branches (a
-  // register array indexed by a runtime value would go to scratch).
-  f32x16 acc;
-  float aself;
-  if (g == 0) { acc = rb[0].o[0]; aself = aw[0]; }
-  else if (g == 1) { acc = rb[0].o[1]; aself = aw[1]; }
-  else if (g == 2) { acc = rb[1].o[0]; aself = aw[2]; }
-  else { acc = rb[1].o[1]; aself = aw[3]; }
-  acc *= aself;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    if (w == g) continue;
-    const int slot = w < g ? w : w - 1;
-    const float* in = ox + (g * 3 + slot) * 16 * 64;
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(in + (r4 * 64 + lane) * 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[4 * r4 + e] += v4[e] * aw[w];
-    }
-  }
-  const float l_tot = sum_xor32(lsum);
-  const float inv = 1.f / l_tot;
-  // Stage the block: lanes l and l^32 hold the two 8-byte halves of each
-  // 16-byte chunk; a permlane32 swap gives each lane whole chunks.
-  const int hi = lane >> 5;
-#pragma unroll
-  for (int gp = 0; gp < 2; ++gp) {
-    uint32_t w2[2][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int gg = 2 * gp + j;
-      const f16x2 a = cvt2x<BF16>(acc[4 * gg + 0] * inv, acc[4 * gg + 1] * inv);
-      const f16x2 b = cvt2x<BF16>(acc[4 * gg + 2] * inv, acc[4 * gg + 3] * inv);
-      w2[j][0] = __builtin_bit_cast(uint32_t, a);
-      w2[j][1] = __builtin_bit_cast(uint32_t, b);
-    }
-    const auto r0 = __builtin_amdgcn_permlane32_swap(w2[0][0], w2[1][0], false, false);
-    const auto r1 = __builtin_amdgcn_permlane32_swap(w2[0][1], w2[1][1], false, false);
-    const int chunk = 4 * dbo + 2 * gp + hi;     // 16-byte chunk of the row
-    *reinterpret_cast<uint4*>(stage + (32 * ro + (lane & 31)) * STAGE_STRIDE + chunk * 16) =
-        uint4{r0[0], r1[0], r0[1], r1[1]};
-  }
-  const int row0 = q0 + 64 * rh;
-  if (WRITE_L && dbo == 0 && hi == 0) {
-    const int qrow = row0 + 32 * ro + (lane & 31);
-    if (FULL || qrow < N) L[hv.l + qrow] = (M + log2_hw(l_tot)) * kLn2;
-  }
-  __syncthreads();
-  // Wave g stores rows 16 g .. 16 g + 15 of the half: 8 lanes per row.
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int idx = 64 * k + lane;
-    const int r = 16 * g + (idx >> 3), ch = idx & 7;
-    const uint4 v = *reinterpret_cast<const uint4*>(stage + r * STAGE_STRIDE + ch * 16);
-    if (FULL || row0 + r < N)
-      *reinterpret_cast<uint4*>(O + head + (size_t)(row0 + r) * D + ch * 8) = v;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Ping-pong kernel: 8 waves. Wave w is row group w % 4 and group w / 4;
@@ -863,11 +459,10 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   };
 
   // Per-lane offsets of the operand fragments within a tile.
-  int koffs[KSTEPS], voffs[DB];
+  int koffs[KSTEPS];
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) koffs[kk] = k_frag_off<D>(kk, lane);
-#pragma unroll
-  for (int db = 0; db < DB; ++db) voffs[db] = v_frag_off<D>(db, lane);
+  const int voff_l = vblk_lane_off(lane);
 
   // Prologue: the waves share the copies of K tiles 0 .. RING-2 and V tiles
   // 0 .. RING-4 (those read before the first M-phase copies land), 1 KiB
@@ -908,19 +503,18 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     uint32_t kt = lds0 + (tq % RING) * TILE;
     uint32_t vt = lds0 + (RING + tv % RING) * TILE;
     asm("" : "+s"(kt), "+s"(vt));
-    lds_cp kl[KSTEPS], vl[DB];
+    lds_cp kl[KSTEPS];
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) kl[kk] = lds_lane_base(kt + koffs[kk]);
-#pragma unroll
-    for (int db = 0; db < DB; ++db) vl[db] = lds_lane_base(vt + voffs[db]);
+    const lds_cp vl = lds_lane_base(vt + voff_l);
     // MFMA m is PV i or QK i: with PV, even m = PV m / 2 and odd m = QK
     // m / 2; without PV, QK m. QK i: block i % NB, k-step i / NB. PV i:
-    // k-step i / DB, d-block i % DB.
+    // k-step i / DB, d-block i % DB: V block i.
     auto is_pv = [](int m) { return PV && (m & 1) == 0; };
     auto idx = [](int m) { return PV ? m >> 1 : m; };
     auto fetch = [&](int m) -> f16x8 {
       const int i = idx(m);
-      if (is_pv(m)) return v_frag_lds<D>(vl[i % DB] + (i / DB) * 16 * 2 * D);
+      if (is_pv(m)) return vblk_frag(vl + i * 1024);
       return lds_b128(kl[i / NB] + (i % NB) * 32 * 2 * D);
     };
     f16x8 op[NM];
@@ -1038,7 +632,11 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       __syncthreads();
     }
     // Phase 2n: the last PV.
-    rb.template pv<NB>(smem + (RING + tile_of(grp, n_steps - 1) % RING) * TILE, 0, p);
+    {
+      const lds_cp vl = lds_lane_base(lds0 + (RING + tile_of(grp, n_steps - 1) % RING) * TILE + voff_l);
+#pragma unroll
+      for (int i = 0; i < NMM; ++i) rb.o[i % DB] = mma32<BF16>(vblk_frag(vl + i * 1024), p[i / DB], rb.o[i % DB]);
+    }
     __syncthreads();
   }
   wait_vmem();   // copies of the last M phases
@@ -1061,19 +659,13 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 }
 
 // Kernel variants (for fa_probe_fwd_variant; the default path picks one per
-// head dimension): 200 + r = ping-pong kernel with a ring of r tiles (D 64
-// and 128); 500 + r = row-pair kernel with a ring of r tiles (D = 64).
+// head dimension): 200 + r = ping-pong kernel with a ring of r tiles.
 constexpr int kPingPong = 204;
-constexpr int kRowPair6 = 506;
-constexpr int kRowPair8 = 508;
 constexpr int kGuarded = 1000;   // probe flag: force the guarded (not full-tile) instance
 
-// Variants that exist for head dimension D and the causal flag (the
-// row-pair kernel is built non-causal only: its diagonal masking would not
-// fit the 256 registers of two waves per SIMD without spilling).
+// Variants that exist for head dimension D and the causal flag.
 static bool variant_fits(int D, int variant, int causal) {
   if (variant == kPingPong) return true;
-  if (variant == kRowPair6 || variant == kRowPair8) return D == 64 && !causal;
   return false;
 }
 
@@ -1090,20 +682,6 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
       hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4>), dim3(total), dim3(512), 0,
                          stream, Q, K, V, Op, lse, geo, num_qb, total, c);
       break;
-    case kRowPair6:
-      if constexpr (D == 64 && !CAUSAL) {
-        hipLaunchKernelGGL((fa_fwd_rp_kernel<CAUSAL, WRITE_L, FULL, 6>), dim3(total), dim3(512), 0,
-                           stream, Q, K, V, Op, lse, geo, num_qb, total, c);
-        break;
-      }
-      return hipErrorInvalidValue;
-    case kRowPair8:
-      if constexpr (D == 64 && !CAUSAL) {
-        hipLaunchKernelGGL((fa_fwd_rp_kernel<CAUSAL, WRITE_L, FULL, 8>), dim3(total), dim3(512), 0,
-                           stream, Q, K, V, Op, lse, geo, num_qb, total, c);
-        break;
-      }
-      return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
   }
@@ -1344,7 +922,7 @@ extern "C" int fa_probe_default_variant(int64_t D) {
 }
 
 extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal) {
-  static const int all[] = {204, 506, 508};
+  static const int all[] = {204};
   int n = 0;
   for (int v : all) {
     if (fa::variant_fits((int)D, v, causal)) {

@@ -54,8 +54,7 @@ int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o, f
                          void* stream);
 
 /* The variant fa_fwd_f16 runs for head dimension D, non-causal (0 for another D):
- * 204 = ping-pong kernel (32 rows per wave, ring of 4 tiles), 506 / 508 =
- * row-pair kernel (D = 64, 64 rows per wave, ring of 6 / 8 tiles). */
+ * 204 = ping-pong kernel (two wave groups, ring of 4 tiles). */
 int fa_probe_default_variant(int64_t D);
 
 /* Writes up to max_out variant codes that exist for head dimension D and the
