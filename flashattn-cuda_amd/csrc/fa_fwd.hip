@@ -39,7 +39,6 @@ namespace fa {
 
 constexpr int kBR = 128;   // query rows per workgroup
 constexpr int kBC = 64;    // keys per tile
-constexpr int kRowGroups = kBR / 32;
 // A lane's tile sum of P above this triggers a rescale; it bounds every P,
 // so P stays far inside the fp16 range (65504).
 constexpr float kSumLimit = 32768.0f;
@@ -375,7 +374,7 @@ __device__ __forceinline__ void dma_block_or_zero(const char* head, int head_byt
 // combine afterwards.
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false,
-          bool SPLITKV = false>
+          bool SPLITKV = false, int TG = 2>
 __global__ void __launch_bounds__(512)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
@@ -385,8 +384,14 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int NB = 2;                        // 32-key blocks per tile
   constexpr int TILE = kBC * D * 2;            // bytes of a 64-key K or V tile
   constexpr int BLOCKS = TILE / 1024;          // 1 KiB blocks per tile
-  constexpr int LOADS = BLOCKS / 4;            // blocks per M-phase wave per tile
-  static_assert(RING % 2 == 0 && RING >= 4, "a ring of whole steps, two at least");
+  constexpr int NRG = 8 / TG;                  // row groups (32 rows each)
+  constexpr int ROWS = 32 * NRG;               // query rows of the workgroup
+  constexpr int LOADS = BLOCKS / NRG;          // blocks per M-phase wave per tile
+  static_assert(TG == 2 || TG == 4, "two or four tile groups");
+  static_assert(!SPLITKV || TG == 2, "split-KV runs with two tile groups");
+  // Two steps of slots: a copy lands one step ahead of its read, and the
+  // prologue's waits below are counted for this ring.
+  static_assert(RING == 2 * TG, "a ring of two steps");
   static_assert(2 * RING * TILE <= 160 * 1024, "slots exceed the 160 KiB LDS");
   using RB = RowBlock<D, CAUSAL, FULL, BF16>;
   constexpr int DB = RB::DB;
@@ -394,17 +399,18 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int NMM = NB * KSTEPS;             // MFMAs of one QK (= of one PV)
   constexpr int PF = D == 64 ? 8 : 4;          // operand prefetch distance, in MFMAs
   constexpr int REC = (2 + 16 * DB) * 64;      // floats per wave record of the merge
-  static_assert(kRowGroups * REC * 4 <= 2 * RING * TILE, "merge area too small");
+  static_assert((TG - 1) * NRG * REC * 4 <= 2 * RING * TILE, "merge area too small");
   // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
   __shared__ __attribute__((aligned(1024))) char smem[2 * RING * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: SGPR
-  const int rg = wave & (kRowGroups - 1);
-  const int grp = wave >> 2;                   // group 0 starts in the S phase
-  // Tile of group g in step j.
-  auto tile_of = [&](int g, int j) { return 2 * j + g; };
+  const int rg = wave % NRG;                   // row group
+  const int tg = wave / NRG;                   // tile group: tiles tg, tg + TG, ...
+  const int grp = tg / (TG / 2);               // phase group; group 0 starts in the S phase
+  // This wave's tile in step j.
+  auto tile_of = [&](int j) { return TG * j + tg; };
 
   const int logical = xcd_remap(blockIdx.x, total);
   // Split-KV: the splits of one q-block are adjacent (same XCD, same K/V).
@@ -416,15 +422,15 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 
   const HeadView hv = head_view<D>(geo, bh);
   const int N = hv.n;
-  if (qb * kBR >= N) return;   // varlen: past this sequence (whole workgroup)
+  if (qb * ROWS >= N) return;   // varlen: past this sequence (whole workgroup)
   const size_t head = hv.q;
   const int head_bytes = N * D * 2;
-  const int q0 = qb * kBR;
+  const int q0 = qb * ROWS;
 
   RB rb;
   rb.init(Q + head, head_bytes, lane, q0 + 32 * rg, N, c);
 
-  const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
+  const int kv_end = CAUSAL ? min(N, q0 + ROWS) : N;
   int n_tiles = (kv_end + kBC - 1) / kBC;
   // Split-KV: this workgroup's tiles are tb .. tb + n_tiles - 1 of the row
   // block's; K/V pointers and bounds start at tile tb, masking uses absolute
@@ -442,7 +448,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int kv_bytes = head_bytes - tb * TILE;
   const char* Kh = reinterpret_cast<const char*>(K + hv.kv) + (size_t)tb * TILE;
   const char* Vh = reinterpret_cast<const char*>(V + hv.kv) + (size_t)tb * TILE;
-  const int n_steps = (n_tiles + 1) / 2;       // tiles per group
+  const int n_steps = (n_tiles + TG - 1) / TG;   // tiles per tile group
 
   const uint32_t lds0 = lds_addr(smem);
   // This wave's share of a tile copy in its M phase: blocks rg*LOADS .. +LOADS.
@@ -464,11 +470,12 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   for (int kk = 0; kk < KSTEPS; ++kk) koffs[kk] = k_frag_off<D>(kk, lane);
   const int voff_l = vblk_lane_off(lane);
 
-  // Prologue: the waves share the copies of K tiles 0 .. RING-2 and V tiles
-  // 0 .. RING-4 (those read before the first M-phase copies land), 1 KiB
-  // block by block.
+  // Prologue: the waves share the copies of K tiles 0 .. RING - TG/2 - 1 and
+  // V tiles 0 .. RING - 3 TG/2 - 1 (those read before the first M-phase
+  // copies land), 1 KiB block by block. (Waiting only for the K tiles of
+  // step 0 here and for the rest during phase 0 measured 1-2% slower.)
   {
-    constexpr int NK = RING - 1, NV = RING - 3;
+    constexpr int NK = RING - TG / 2, NV = RING - 3 * TG / 2;
     constexpr int ITEMS = (NK + NV) * BLOCKS;
 #pragma unroll
     for (int it0 = 0; it0 < ITEMS; it0 += 8) {
@@ -549,7 +556,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       // the next split, so masking by N would not remove them. P = 0.
 #pragma unroll
       for (int j = 0; j < 2 * NB; ++j) p[j] = f16x8{};
-      wait_vmcnt<(RING / 2 - 2) * 2 * LOADS>();
+      wait_vmcnt<((RING - TG) / TG - 1) * 2 * LOADS>();
       return;
     }
     rb.template mask<2>(tb + t, 0, s);
@@ -580,9 +587,9 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     float rs = acc[0] + acc[1];
     if (__builtin_expect(!__all(rs <= kSumLimit), 0)) rs = rb.template rescue<NB>(s, p);
     rb.l_run += rs;
-    // This wave's copies of its M phase RING/2 - 1 phases of its own back;
-    // those of the later M phases stay in flight.
-    wait_vmcnt<(RING / 2 - 2) * 2 * LOADS>();
+    // This wave's copies of its M phase (RING - TG) / TG steps back; those of
+    // the later M phases stay in flight.
+    wait_vmcnt<((RING - TG) / TG - 1) * 2 * LOADS>();
   };
 
   // A phase's register-only work must stay between its barriers: the compiler
@@ -597,19 +604,21 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int j = 0; j < 2 * NB; ++j) asm volatile("" : "+v"(p[j]));
   };
-  // M phase copies: K and V of the tiles RING - 2 after the ones it reads.
+  // M phase copies: K and V of the tiles RING - TG after the ones it reads
+  // (the same tile group's tiles one ring turn minus a step later), into the
+  // slots of the tiles it read in its previous M phase.
   auto mstep = [&](auto with_pv, int tq, int tv) {
-    mphase(with_pv, tq, tv, tq + RING - 2, tv + RING - 2);
+    mphase(with_pv, tq, tv, tq + RING - TG, tv + RING - TG);
   };
   if (grp == 0) {
-    rb.template qk<NB>(smem + (tile_of(grp, 0) % RING) * TILE, 0, s);
+    rb.template qk<NB>(smem + (tile_of(0) % RING) * TILE, 0, s);
     __syncthreads();                 // its slot is refilled in phase 1
     for (int j = 0; j < n_steps; ++j) {
       pin_s();
-      sphase(tile_of(grp, j));
+      sphase(tile_of(j));
       pin_p();
       __syncthreads();
-      mstep(BT{}, tile_of(grp, j + 1), tile_of(grp, j));
+      mstep(BT{}, tile_of(j + 1), tile_of(j));
       __syncthreads();
     }
     __syncthreads();   // group 1's last PV
@@ -617,23 +626,23 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     __syncthreads();
     // Step 0 (no PV yet) is peeled: with both M-phase forms in one loop body
     // the compiler moved the accumulators between them on every step.
-    mstep(BF{}, tile_of(grp, 0), tile_of(grp, -1));
+    mstep(BF{}, tile_of(0), tile_of(-1));
     __syncthreads();
     pin_s();
-    sphase(tile_of(grp, 0));
+    sphase(tile_of(0));
     pin_p();
     __syncthreads();
     for (int j = 1; j < n_steps; ++j) {
-      mstep(BT{}, tile_of(grp, j), tile_of(grp, j - 1));
+      mstep(BT{}, tile_of(j), tile_of(j - 1));
       __syncthreads();
       pin_s();
-      sphase(tile_of(grp, j));
+      sphase(tile_of(j));
       pin_p();
       __syncthreads();
     }
     // Phase 2n: the last PV.
     {
-      const lds_cp vl = lds_lane_base(lds0 + (RING + tile_of(grp, n_steps - 1) % RING) * TILE + voff_l);
+      const lds_cp vl = lds_lane_base(lds0 + (RING + tile_of(n_steps - 1) % RING) * TILE + voff_l);
 #pragma unroll
       for (int i = 0; i < NMM; ++i) rb.o[i % DB] = mma32<BF16>(vblk_frag(vl + i * 1024), p[i / DB], rb.o[i % DB]);
     }
@@ -641,14 +650,16 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   }
   wait_vmem();   // copies of the last M phases
 
-  // Merge group 1 into group 0 through LDS (the ring is free: all copies
-  // have landed and every read is done).
-  float* area = reinterpret_cast<float*>(smem) + rg * REC;
+  // Merge tile groups 1 .. TG-1 into tile group 0 through LDS (the ring is
+  // free: all copies have landed and every read is done).
+  float* area = reinterpret_cast<float*>(smem);
   __syncthreads();
-  if (grp > 0) rb.save_to(area);
+  if (tg > 0) rb.save_to(area + ((tg - 1) * NRG + rg) * REC);
   __syncthreads();
-  if (grp > 0) return;
-  rb.merge_from(area);
+  if (tg > 0) return;
+#pragma unroll
+  for (int g = 1; g < TG; ++g) rb.merge_from(area + ((g - 1) * NRG + rg) * REC);
+  area += rg * REC;   // this wave's first record, read: it stages the O tile
   if constexpr (SPLITKV) {
     rb.finish_partial(part_o, part_lse, (hv.l + rb.qrow) * nsplit + split);
   } else {
@@ -659,13 +670,23 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 }
 
 // Kernel variants (for fa_probe_fwd_variant; the default path picks one per
-// head dimension): 200 + r = ping-pong kernel with a ring of r tiles.
+// problem shape): the ping-pong kernel with two tile groups over 128 rows and
+// a ring of 4 tiles (204), or with four tile groups over 64 rows and a ring
+// of 8 tiles (408, D = 64: twice the workgroups for the same rows).
 constexpr int kPingPong = 204;
+constexpr int kPingPong4 = 408;
 constexpr int kGuarded = 1000;   // probe flag: force the guarded (not full-tile) instance
+
+// Query rows per workgroup, and the multiple of N that lets every tile group
+// run the same number of whole tiles (the full-tile instance).
+static int variant_rows(int variant) { return variant == kPingPong4 ? 64 : kBR; }
+static int variant_full_n(int variant) { return variant == kPingPong4 ? 256 : kBR; }
 
 // Variants that exist for head dimension D and the causal flag.
 static bool variant_fits(int D, int variant, int causal) {
+  (void)causal;
   if (variant == kPingPong) return true;
+  if (variant == kPingPong4) return D == 64;
   return false;
 }
 
@@ -682,6 +703,13 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
       hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4>), dim3(total), dim3(512), 0,
                          stream, Q, K, V, Op, lse, geo, num_qb, total, c);
       break;
+    case kPingPong4:
+      if constexpr (D == 64) {
+        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, false, false, 4>),
+                           dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
+        break;
+      }
+      return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
   }
@@ -700,12 +728,23 @@ static hipError_t dispatch_wl(const void* q, const void* k, const void* v, void*
               : launch_fwd<D, CAUSAL, false, false>(q, k, v, o, lse, geo, num_qb, total, c, variant, s);
 }
 
-// The kernel the forward runs for head dimension D and the causal flag
-// (measured on MI355X; see bench.py). Fixed per build: nothing in the
-// environment changes it.
-static int choose_variant(int64_t D, int causal) {
-  (void)D;
-  (void)causal;
+constexpr int kNumCUs = 256;   // MI355X
+
+// The kernel the forward runs for a problem shape (bh = B * H heads of N
+// rows), fixed per build: nothing in the environment changes it. Measured on
+// MI355X (D = 64, us, 128-row vs 64-row workgroups): where the 128-row grid
+// leaves CUs idle the 64-row kernel wins (B1 H8 N2048 17.3 -> 13.8, B1 H4
+// N4096 29.7 -> 22.9, B1 H16 N1024 11.3 -> 9.6), and so it does for causal
+// long rows on a single wave of workgroups (B1 H8 N4096 33.6 -> 29.0, the
+// short row blocks finish early and free their CUs); from 256 row blocks
+// of 128 on (non-causal) or 512 (causal) it loses (B1 H16 N2048 21.1 vs 26.5,
+// B2 H8 N4096 causal 45.1 vs 55.5), as it does for causal N = 1024 (B4 H8
+// 12.8 vs 17.6).
+static int choose_variant(int64_t D, int causal, int64_t bh, int64_t N) {
+  if (D != 64) return kPingPong;
+  const int64_t grid = bh * ((N + kBR - 1) / kBR);
+  if (grid < kNumCUs) return kPingPong4;
+  if (causal && grid == kNumCUs && N >= 2048) return kPingPong4;
   return kPingPong;
 }
 
@@ -720,12 +759,15 @@ static int fwd_run(const void* q, const void* k, const void* v, void* o, float* 
   // multiple of the row block (tests compare it bitwise with the full-tile one).
   const bool guarded = variant >= kGuarded;
   if (guarded) variant -= kGuarded;
-  if (variant == 0) variant = choose_variant(D, causal);
+  if (variant == 0) variant = choose_variant(D, causal, B * geo.H, geo.N);
   if (!variant_fits((int)D, variant, causal)) return FA_ERR_HEAD_DIM;
-  const int num_qb = (geo.N + kBR - 1) / kBR;
+  const int rows = variant_rows(variant);
+  const int num_qb = (geo.N + rows - 1) / rows;
+  // The validation bounds the grid of 128-row blocks; 64-row blocks double it.
+  if (B * geo.H * (int64_t)num_qb > (int64_t(1) << 31) - 1) return FA_ERR_TOO_LARGE;
   const int total = (int)(B * geo.H * num_qb);
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
-  const bool full = !guarded && geo.cu == nullptr && (geo.N % kBR) == 0;
+  const bool full = !guarded && geo.cu == nullptr && (geo.N % variant_full_n(variant)) == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   if (D == 64) {
@@ -750,7 +792,6 @@ static int fwd_dense(const void* q, const void* k, const void* v, void* o, float
 }  // namespace fa
 
 namespace fa {
-constexpr int kNumCUs = 256;   // MI355X
 
 // Split-KV forward: the ping-pong kernel over (row block, split) units writes
 // normalised fp32 partials and their LSEs; the decode's LSE combine, over the
@@ -778,6 +819,11 @@ extern "C" int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, i
   // dominate (B1 H8 N1024: 11.5 -> 12.8 us + 7 us), and causal triangles did
   // not even out (B1 H8 N4096 causal: 36.5 -> 42.6 us).
   if (causal) return 1;
+  // D = 64: the 64-row kernel (chosen where 128-row blocks leave CUs idle)
+  // beat every split count (us: B1 H1 N16384 79.7 vs 85.6 with 2 splits, B1 H2
+  // N8192 42.0 vs 49.5, B1 H1 N8192 31.6 vs 32.0 with 4, B1 H2 N4096 18.8 vs
+  // 23.1 with 4).
+  if (D == 64) return 1;
   const int64_t units = B * H * ((N + fa::kBR - 1) / fa::kBR);
   const int64_t tiles = (N + fa::kBC - 1) / fa::kBC;   // key tiles of a row block
   if (units >= fa::kNumCUs) return 1;
@@ -918,11 +964,11 @@ extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v,
 
 extern "C" int fa_probe_default_variant(int64_t D) {
   if (D != 64 && D != 128) return 0;
-  return fa::choose_variant(D, 0);
+  return fa::choose_variant(D, 0, 8, 4096);
 }
 
 extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal) {
-  static const int all[] = {204};
+  static const int all[] = {204, 408};
   int n = 0;
   for (int v : all) {
     if (fa::variant_fits((int)D, v, causal)) {

@@ -53,8 +53,11 @@ int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o, f
                          int64_t B, int64_t H, int64_t N, int64_t D, int causal, int variant,
                          void* stream);
 
-/* The variant fa_fwd_f16 runs for head dimension D, non-causal (0 for another D):
- * 204 = ping-pong kernel (two wave groups, ring of 4 tiles). */
+/* The variant fa_fwd_f16 runs for head dimension D at the headline shape
+ * (B = 1, H = 8, N = 4096, non-causal; 0 for another D). 204 = ping-pong
+ * kernel with two tile groups over 128 rows (ring of 4 tiles), 408 = with
+ * four tile groups over 64 rows (ring of 8 tiles, D = 64); the forward picks
+ * 408 for D = 64 where 128-row workgroups leave CUs idle. */
 int fa_probe_default_variant(int64_t D);
 
 /* Writes up to max_out variant codes that exist for head dimension D and the
