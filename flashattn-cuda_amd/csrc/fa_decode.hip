@@ -237,7 +237,12 @@ fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
 // used for all G heads (a lane's dot products, softmax state and output
 // slice are kept per head), so a page is read once per KV head instead of
 // once per query head. Waves split the pages as above and merge per head.
-template <int D, int G, bool BF16>
+//
+// LPT lanes share a token: with LPT = 4 a lane holds D / 4 columns of one
+// token of the page; with LPT = 8 it holds D / 8 columns of two tokens
+// (t and t + 8), which halves the per-head query and output registers so
+// that four heads fit at D = 128.
+template <int D, int G, bool BF16, int LPT = 4>
 __global__ void __launch_bounds__(kDecThreads)
 fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
                              const typename DecT<BF16>::e* __restrict__ kpool,
@@ -249,8 +254,10 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
   using T = DecT<BF16>;
   using v8 = typename T::v8;
   using v2 = typename T::v2;
-  constexpr int DPL = D / 4;   // d per lane
-  constexpr int NV = DPL / 8;  // 16-byte vectors per lane per row
+  static_assert(LPT == 4 || LPT == 8, "4 or 8 lanes per token");
+  constexpr int DPL = D / LPT;   // d per lane
+  constexpr int NV = DPL / 8;    // 16-byte vectors per lane per row
+  constexpr int TPL = LPT / 4;   // tokens per lane: tok + 8 j
   __shared__ float sh_o[kDecWaves][G][D];
   __shared__ float sh_m[kDecWaves][G];
   __shared__ float sh_l[kDecWaves][G];
@@ -263,8 +270,8 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
   const int h0 = hg * G;                  // first query head of this workgroup
   const int hk = h0 / (H / Hkv);          // their KV head (G divides H / Hkv)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tok = lane >> 2;
-  const int dq = lane & 3;
+  const int tok = lane / LPT;
+  const int dq = lane % LPT;
 
   if (tid == 0) sh_bad = 0;
   __syncthreads();
@@ -305,42 +312,66 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
     const int pid = pt[p];
     if (pid < 0 || pid >= num_pages) { bad = true; continue; }
     const size_t base = ((size_t)pid * Hkv + hk) * (kPage * D) + (size_t)tok * D + dq * DPL;
-    v8 kv[NV], vv[NV];
+    v8 kv[TPL][NV], vv[TPL][NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) kv[i] = *reinterpret_cast<const v8*>(kpool + base + 8 * i);
+    for (int j = 0; j < TPL; ++j) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) vv[i] = *reinterpret_cast<const v8*>(vpool + base + 8 * i);
-    const bool live = p * kPage + tok < ctx;
-    if (!live) {   // slot past the context: drop its V row (it may hold NaN or Inf)
+      for (int i = 0; i < NV; ++i) kv[j][i] = *reinterpret_cast<const v8*>(kpool + base + j * 8 * D + 8 * i);
+    }
 #pragma unroll
-      for (int i = 0; i < NV; ++i) vv[i] = v8{};
+    for (int j = 0; j < TPL; ++j) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) vv[j][i] = *reinterpret_cast<const v8*>(vpool + base + j * 8 * D + 8 * i);
+    }
+    bool live[TPL];
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) {
+      live[j] = p * kPage + tok + 8 * j < ctx;
+      if (!live[j]) {   // slot past the context: drop its V row (it may hold NaN or Inf)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) vv[j][i] = v8{};
+      }
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float dot = 0.f;
+      float st[TPL];
+      float mp = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
+      for (int j = 0; j < TPL; ++j) {
+        float dot = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dot = T::dot2(qv[g][4 * i + e], v2{kv[i][2 * e], kv[i][2 * e + 1]}, dot);
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dot = T::dot2(qv[g][4 * i + e], v2{kv[j][i][2 * e], kv[j][i][2 * e + 1]}, dot);
+          }
         }
+#pragma unroll
+        for (int sh = 1; sh < LPT; sh <<= 1) dot += __shfl_xor(dot, sh, 64);
+        st[j] = live[j] ? dot * c : -INFINITY;
+        mp = fmaxf(mp, st[j]);
       }
-      dot += __shfl_xor(dot, 1, 64);
-      dot += __shfl_xor(dot, 2, 64);
-      const float st = live ? dot * c : -INFINITY;
-      float mp = st;
-      mp = fmaxf(mp, __shfl_xor(mp, 4, 64));
-      mp = fmaxf(mp, __shfl_xor(mp, 8, 64));
-      mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
-      mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+#pragma unroll
+      for (int sh = LPT; sh < 64; sh <<= 1) mp = fmaxf(mp, __shfl_xor(mp, sh, 64));
       const float m_new = fmaxf(m[g], mp);   // finite: token p*16 < ctx
       const float alpha = (m_new == m[g]) ? 1.f : exp2_hw(m[g] - m_new);
-      const float pr = exp2_hw(st - m_new);
-      l[g] = l[g] * alpha + pr;
+      float pr[TPL];
+      float psum = 0.f;
+#pragma unroll
+      for (int j = 0; j < TPL; ++j) {
+        pr[j] = exp2_hw(st[j] - m_new);
+        psum += pr[j];
+      }
+      l[g] = l[g] * alpha + psum;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][8 * i + e] = fmaf(pr, (float)vv[i][e], o[g][8 * i + e] * alpha);
+        for (int e = 0; e < 8; ++e) {
+          float acc = o[g][8 * i + e] * alpha;
+#pragma unroll
+          for (int j = 0; j < TPL; ++j) acc = fmaf(pr[j], (float)vv[j][i][e], acc);
+          o[g][8 * i + e] = acc;
+        }
       }
       m[g] = m_new;
     }
@@ -349,7 +380,7 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
 #pragma unroll
   for (int g = 0; g < G; ++g) {
 #pragma unroll
-    for (int sh = 4; sh < 64; sh <<= 1) {
+    for (int sh = LPT; sh < 64; sh <<= 1) {
       l[g] += __shfl_xor(l[g], sh, 64);
 #pragma unroll
       for (int i = 0; i < DPL; ++i) o[g][i] += __shfl_xor(o[g][i], sh, 64);
@@ -446,22 +477,22 @@ static int decode_split(const void* q, const void* k_pool, const void* v_pool,
   const E* Kp = (const E*)k_pool;
   const E* Vp = (const E*)v_pool;
   // Grouped KV heads: G query heads per workgroup share each page read. At
-  // D = 128 four heads' state needs 256 VGPRs (one wave per SIMD, too few to
-  // stream HBM), so G stays at 2 there (measured: group-of-4 pools at 507 µs
-  // with G = 2 vs 706 µs with G = 4 and 750 µs with G = 1).
+  // D = 128 four heads take 8 lanes per token (two tokens per lane), which
+  // keeps their state within the registers of three waves per SIMD; with 4
+  // lanes per token they needed 256 VGPRs (one wave per SIMD: 706 us vs 507 us
+  // for G = 2 on the group-of-4 pools).
   const int64_t group = H / Hkv;
-  const int maxg = D == 128 ? 2 : 4;
-  const int G = (group % 4 == 0 && maxg >= 4) ? 4 : (group % 2 == 0 ? 2 : 1);
+  const int G = group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
   if (G > 1) {
     const dim3 ggrid((unsigned)num_splits, (unsigned)(H / G), (unsigned)B);
-#define FA_DEC_GROUP(DD, GG)                                                                    \
-  hipLaunchKernelGGL((fa_decode_split_group_kernel<DD, GG, BF16>), ggrid, dim3(kDecThreads), 0, \
-                     s, Q, Kp, Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,     \
+#define FA_DEC_GROUP(DD, GG, LL)                                                                    \
+  hipLaunchKernelGGL((fa_decode_split_group_kernel<DD, GG, BF16, LL>), ggrid, dim3(kDecThreads), 0, \
+                     s, Q, Kp, Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,         \
                      (int)max_pages, (int)num_pages, (int)num_splits, c)
     if (D == 128) {
-      FA_DEC_GROUP(128, 2);
+      if (G == 4) FA_DEC_GROUP(128, 4, 8); else FA_DEC_GROUP(128, 2, 4);
     } else {
-      if (G == 4) FA_DEC_GROUP(64, 4); else FA_DEC_GROUP(64, 2);
+      if (G == 4) FA_DEC_GROUP(64, 4, 4); else FA_DEC_GROUP(64, 2, 4);
     }
 #undef FA_DEC_GROUP
     hipError_t e = hipGetLastError();
