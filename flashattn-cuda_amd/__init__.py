@@ -69,6 +69,7 @@ def forward_varlen(q, k, v, cu_seqlens, max_seqlen: int, causal: bool = False):
 
     Sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1] (int32 [B+1]) of every
     head and attends only within itself; max_seqlen must cover every sequence.
+    Rows past cu_seqlens[B] belong to no sequence: O = 0 and L = -inf there.
     """
     return _C.forward_varlen(q, k, v, cu_seqlens, max_seqlen, causal)
 

@@ -13,6 +13,8 @@
 // include/fa_mi355x.h; this file makes no HIP call of its own.
 #include <torch/extension.h>
 
+#include <limits>
+
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
@@ -155,8 +157,11 @@ std::vector<torch::Tensor> forward_varlen(torch::Tensor q, torch::Tensor k, torc
   auto kh = k.to(torch::kHalf).contiguous();
   auto vh = v.to(torch::kHalf).contiguous();
   auto cu = cu_seqlens.contiguous();
+  // Rows outside every sequence (past cu_seqlens[B]) are not written by the
+  // kernel: they keep O = 0 and L = -inf, the logsumexp of no keys.
   auto O = torch::zeros({H, total, D}, qh.options());
-  auto L = torch::empty({H, total}, qh.options().dtype(torch::kFloat));
+  auto L = torch::full({H, total}, -std::numeric_limits<float>::infinity(),
+                       qh.options().dtype(torch::kFloat));
   const int st = fa_fwd_varlen_f16(qh.data_ptr(), kh.data_ptr(), vh.data_ptr(), O.data_ptr(),
                                    L.data_ptr<float>(), cu.data_ptr<int32_t>(), B, H, Hkv,
                                    max_seqlen, total, D, causal ? 1 : 0, current_stream(qh));

@@ -97,13 +97,16 @@ def test_varlen_single_sequence_matches_dense(fa, dev):
 
 
 def test_varlen_rows_outside_sequences_and_malformed_bounds(fa, dev):
-    """Trailing rows past cu[B] stay zero; out-of-range bounds are clamped."""
+    """Trailing rows past cu[B] keep O = 0 and L = -inf (an empty sequence
+    adds no rows); out-of-range bounds are clamped."""
     H, D = 2, 64
     total = 300
     q, k, v = (torch.from_numpy(_randn((H, total, D), s)).to(dev).half() for s in (13, 14, 15))
-    cu = torch.tensor([0, 100, 200], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 100, 100, 200], dtype=torch.int32, device=dev)
     O, L = fa.forward_varlen(q, k, v, cu, 100)
     assert torch.count_nonzero(O[:, 200:]).item() == 0
+    assert torch.isneginf(L[:, 200:]).all()
+    assert torch.isfinite(L[:, :200]).all()
     # decreasing and past-the-end bounds: nothing is read or written outside
     bad = torch.tensor([0, 250, 100, 10_000], dtype=torch.int32, device=dev)
     O2, _ = fa.forward_varlen(q, k, v, bad, 256)
