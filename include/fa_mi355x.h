@@ -142,7 +142,7 @@ int fa_validate_bwd(const void* q, const void* k, const void* v, const void* o,
                     const float* dv, const float* workspace, int64_t B, int64_t H,
                     int64_t N, int64_t D);
 
-/* Floats of the workspace fa_bwd_f16 needs: 2*B*H*N (the row sums D_i, then -lse*log2(e)). */
+/* Floats of the workspace fa_bwd_f16 needs: 2*B*H*N (the negated row sums -D_i, then -lse*log2(e)). */
 int64_t fa_bwd_workspace_floats(int64_t B, int64_t H, int64_t N);
 
 /*
