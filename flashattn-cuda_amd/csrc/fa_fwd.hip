@@ -191,6 +191,13 @@ struct RowBlock {
     return expo_pack<NB>(s, pf, m_safe());
   }
 
+  // Merge records in LDS: m and l of the 64 lanes, then O in groups of four
+  // registers, lane-major (16 bytes per lane, 1 KiB per group), so a lane
+  // writes and reads its O with 16-byte accesses (conflict-free: the 64
+  // lanes of an access cover 1 KiB contiguously).
+  static constexpr int REC_FLOATS = (2 + 16 * DB) * 64;
+  __device__ __forceinline__ static int rec_o(int g, int lane) { return 128 + (g * 64 + lane) * 4; }
+
   // Merge another wave's (m, l, O) for the same rows, read from LDS.
   __device__ __forceinline__ void merge_from(const float* src) {
     const float m2 = src[lane];
@@ -202,7 +209,11 @@ struct RowBlock {
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a1 + src[(2 + 16 * db + r) * 64 + lane] * a2;
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + rec_o(4 * db + q, lane));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[db][4 * q + e] = o[db][4 * q + e] * a1 + v[e] * a2;
+      }
     }
     m_run = M;
   }
@@ -213,7 +224,9 @@ struct RowBlock {
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dst[(2 + 16 * db + r) * 64 + lane] = o[db][r];
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(dst + rec_o(4 * db + q, lane)) =
+            f32x4{o[db][4 * q], o[db][4 * q + 1], o[db][4 * q + 2], o[db][4 * q + 3]};
     }
   }
 
@@ -398,7 +411,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int KSTEPS = D / 16;
   constexpr int NMM = NB * KSTEPS;             // MFMAs of one QK (= of one PV)
   constexpr int PF = D == 64 ? 8 : 4;          // operand prefetch distance, in MFMAs
-  constexpr int REC = (2 + 16 * DB) * 64;      // floats per wave record of the merge
+  constexpr int REC = RB::REC_FLOATS;          // floats per wave record of the merge
   static_assert((TG - 1) * NRG * REC * 4 <= 2 * RING * TILE, "merge area too small");
   // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
   __shared__ __attribute__((aligned(1024))) char smem[2 * RING * TILE];
