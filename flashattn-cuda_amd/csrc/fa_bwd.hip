@@ -260,27 +260,26 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
   }
 
   // Block b = i * WAVES + wave of a stage: part b / BLOCKS of {Qk, Qv, dOk,
-  // dOv}, block b % BLOCKS of that tile.
-  uint32_t off[LOADS];
-#pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int b = i * WAVES + wave;
-    uint32_t ko, vo;
-    block_offsets<D>(b % BLOCKS, lane, ko, vo);
-    off[i] = ((b / BLOCKS) & 1) ? vo : ko;
-  }
+  // dOv}, block b % BLOCKS of that tile. The per-lane source offsets are
+  // recomputed at each copy from a lane id the compiler cannot hoist: held
+  // across the loop they are the first registers spilled at D = 128, and a
+  // reload before each copy waits for every copy before it.
   const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int t, int st) {
     const uint32_t base = lds0 + st * STAGE;
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int b = i * WAVES + wave;
       const int part = b / BLOCKS;
+      uint32_t ko, vo;
+      block_offsets<D>(b % BLOCKS, ln, ko, vo);
       copy_block<D>(part < 2 ? Qh : Gh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
-                    off[i]);
+                    (part & 1) ? vo : ko);
     }
-    if (wave == 0) copy_rowvec(Lh, N, t, base + 4 * TILE, lane);
-    if (wave == 1) copy_rowvec(Dh, N, t, base + 4 * TILE + 1024, lane);
+    if (wave == 0) copy_rowvec(Lh, N, t, base + 4 * TILE, ln);
+    if (wave == 1) copy_rowvec(Dh, N, t, base + 4 * TILE + 1024, ln);
   };
 
   // One 32-query block qb of the tile at sb: S = Q K^T and dP = dO V^T
@@ -300,6 +299,8 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
     for (int kk = 0; kk < KSTEPS; ++kk) {
       s = mma32<BF16>(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
       dp = mma32<BF16>(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
+      // D = 128: bound the operand reads in flight (registers are the limit)
+      if constexpr (D == 128) if (kk % 2 == 1) __builtin_amdgcn_sched_barrier(0);
     }
     mid();
     f32x16 p, g;
@@ -310,10 +311,14 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
       for (int e = 0; e < 4; ++e) p[4 * r4 + e] = exp2_hw(fmaf(s[4 * r4 + e], c, lq[e]));
     }
     if (edge) {   // rows past N, and (causal) keys after the row
+      // Register r holds query base + 8 (r/4) + r%4: compare that constant
+      // offset against two per-lane limits.
+      const int base = qt0 + 32 * qb + 4 * hi;
+      const int lim_n = N - base, lim_k = key - base;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int q = qt0 + 32 * qb + 8 * (r >> 2) + 4 * hi + (r & 3);
-        p[r] = ((q >= N) || (CAUSAL && key > q)) ? 0.f : p[r];
+        const int ro = 8 * (r >> 2) + (r & 3);
+        p[r] = ((ro >= lim_n) || (CAUSAL && ro < lim_k)) ? 0.f : p[r];
       }
     }
 #pragma unroll
@@ -432,24 +437,20 @@ __device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[0][db] = f32x16{};
 
-  uint32_t off[LOADS];
-#pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int b = i * WAVES + wave;
-    uint32_t ko, vo;
-    block_offsets<D>(b % BLOCKS, lane, ko, vo);
-    off[i] = ((b / BLOCKS) == 1) ? vo : ko;
-  }
   const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](int t, int st) {
+  auto issue = [&](int t, int st) {   // offsets recomputed per copy (see the dK/dV body)
     const uint32_t base = lds0 + st * STAGE;
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int b = i * WAVES + wave;
       if (b < NBLK) {   // wave-uniform
         const int part = b / BLOCKS;
+        uint32_t ko, vo;
+        block_offsets<D>(b % BLOCKS, ln, ko, vo);
         copy_block<D>(part < 2 ? Kh : Vh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
-                      off[i]);
+                      part == 1 ? vo : ko);
       }
     }
   };
@@ -1004,12 +1005,17 @@ fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
   reinterpret_cast<f32x4*>(out)[i4] = acc;
 }
 
+// Units per half below which the D = 128 causal backward runs fused: two
+// per CU of MI355X's 256 (measured crossover, see launch_bwd).
+constexpr int kFuseUnitsD128 = 512;
+
 // Wave groups per workgroup: two (the second group takes the other half of
 // every tile, so the grid stays one workgroup per 128 rows and the SIMDs get
-// a second wave to overlap). At D = 128 the dK/dV body then needs more than
-// the 256 VGPRs two waves per SIMD allow and spills 10 of them (36 bytes of
-// scratch per lane); measured on B4 H16 N4096 causal it still beats one group
+// a second wave to overlap). At D = 128 the dK/dV body then fills the 256
+// VGPRs two waves per SIMD allow (no spill once the copy offsets are
+// recomputed per copy); measured on B4 H16 N4096 causal, two groups beat one
 // (281 VGPRs, one wave per SIMD) by 9%.
+
 template <int D>
 constexpr int kDkdvGroups = 2;
 template <int D>
@@ -1044,13 +1050,20 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const int total = (int)(units * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
   bool launched = false;
-  // One launch where it pays (measured): at D = 64 always, at D = 128 for
-  // causal heads (B1 H8 N4096: 0.255 -> 0.186 ms), not for non-causal ones
-  // (B4 H16 N4096: 2.36 -> 2.50 ms), whose units are all the same length.
+  // One launch where it pays (measured): at D = 64 always; at D = 128 only
+  // for causal heads with fewer units per half than two per CU, where one
+  // wave of workgroups cannot even out the triangle (B1 H8 N4096: 0.237 ->
+  // 0.165 ms). From 512 units on the two launches win (B2 H8 N4096 causal
+  // 307 -> 304 us, B4 H16 N4096 causal 1267 -> 1237 us), and so they do for
+  // non-causal heads (B4 H16 N4096: 2.36 vs 2.50 ms), whose units are all
+  // the same length. (The fused D = 128 body also needs 4 VGPRs more than
+  // the two budgets allow and spills them; the separate kernels do not.)
   if constexpr (GK == 2 && GQ == 2 && (D == 64 || CAUSAL)) {
-    hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
-                       s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
-    launched = true;
+    if (D == 64 || total < kFuseUnitsD128) {
+      hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
+                         s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
+      launched = true;
+    }
   }
   if (!launched) {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
