@@ -280,7 +280,8 @@ __device__ __forceinline__ f16x2 cvt2(float a, float b) {
 template <bool BF16>
 __device__ __forceinline__ f16x2 cvt2x(float a, float b) {
   if constexpr (BF16) {
-    return __builtin_bit_cast(f16x2, bf16x2{(__bf16)a, (__bf16)b});
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(f16x2, __builtin_convertvector(f32x2_t{a, b}, bf16x2));
   } else {
     return cvt2(a, b);
   }
