@@ -158,6 +158,25 @@ def test_headline_shape(fa, dev, D, causal):
     np.testing.assert_allclose(dK.sum(axis=2), 0, atol=2e-3 * scale)
 
 
+def test_causal_d128_two_launch_grid(fa, dev):
+    """D = 128 causal with 512 units per half (B2 H8 N4096): the grid size at
+    which the backward runs the separate dK/dV and dQ kernels instead of the
+    fused launch. Two heads against the oracle, every head through the
+    identities of test_headline_shape."""
+    B, H, N, D = 2, 8, 4096, 128
+    Q, K, V, G = _randn(B, H, N, D, 77)
+    got = _grads(fa, dev, Q, K, V, G, True)
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        bs, hs = slice(b, b + 1), slice(h, h + 1)
+        ref = naive_attention_backward(half_cast(Q[bs, hs]), half_cast(K[bs, hs]),
+                                       half_cast(V[bs, hs]), half_cast(G[bs, hs]), True)
+        _compare([g[bs, hs] for g in got], ref, TIGHT_ATOL, TIGHT_RTOL, f"b{b} h{h}")
+    dQ, dK, dV = got
+    scale = np.sqrt(N)
+    np.testing.assert_allclose(dV.sum(axis=2), half_cast(G).sum(axis=2), atol=2e-3 * scale)
+    np.testing.assert_allclose(dK.sum(axis=2), 0, atol=2e-3 * scale)
+
+
 def test_rejects_bad_arguments(fa, dev):
     x = torch.zeros(1, 1, 8, 64, device=dev)
     L = torch.zeros(1, 1, 8, device=dev)
