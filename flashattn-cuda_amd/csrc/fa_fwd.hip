@@ -385,9 +385,19 @@ __device__ __forceinline__ void dma_block_or_zero(const char* head, int head_byt
 // SPLITKV: the grid covers (row block, key range) units; each writes fp32
 // partials normalised over its range and the range's LSE, merged by the LSE
 // combine afterwards.
+//
+// PAIR (causal, four tile groups): workgroup i of a head owns row blocks
+// A = num_qb - 1 - i and B = i, whose triangles add up to num_qb + 1 tiles,
+// so every workgroup of the grid has the same work. One pipeline runs over
+// A's tiles (rounded up to whole steps, the extra ones past A's diagonal
+// and masked) and then B's: step jb's matrix phase does A's last PV and B's
+// first QK, and each wave then keeps A's state aside until the merge, where
+// tile group 0 finishes A and tile group 1 finishes B. No second prologue,
+// pipeline fill and drain, or workgroup launch per row block; one loop body
+// serves both blocks (a second copy of the loop ran cold and slower).
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false,
-          bool SPLITKV = false, int TG = 2>
+          bool SPLITKV = false, int TG = 2, bool PAIR = false>
 __global__ void __launch_bounds__(512)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
@@ -402,6 +412,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int LOADS = BLOCKS / NRG;          // blocks per M-phase wave per tile
   static_assert(TG == 2 || TG == 4, "two or four tile groups");
   static_assert(!SPLITKV || TG == 2, "split-KV runs with two tile groups");
+  static_assert(!PAIR || (CAUSAL && TG == 4 && !SPLITKV), "row-block pairs: causal, four tile groups");
   // Two steps of slots: a copy lands one step ahead of its read, and the
   // prologue's waits below are counted for this ring.
   static_assert(RING == 2 * TG, "a ring of two steps");
@@ -412,7 +423,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int NMM = NB * KSTEPS;             // MFMAs of one QK (= of one PV)
   constexpr int PF = D == 64 ? 8 : 4;          // operand prefetch distance, in MFMAs
   constexpr int REC = RB::REC_FLOATS;          // floats per wave record of the merge
-  static_assert((TG - 1) * NRG * REC * 4 <= 2 * RING * TILE, "merge area too small");
+  static_assert((PAIR ? 2 : 1) * (TG - 1) * NRG * REC * 4 <= 2 * RING * TILE, "merge area too small");
   // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
   __shared__ __attribute__((aligned(1024))) char smem[2 * RING * TILE];
 
@@ -429,9 +440,12 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // Split-KV: the splits of one q-block are adjacent (same XCD, same K/V).
   const int split = SPLITKV ? logical % nsplit : 0;
   const int unit = SPLITKV ? logical / nsplit : logical;
-  const int bh = unit / num_qb;
-  int qb = unit - bh * num_qb;
-  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
+  const int per_head = PAIR ? (num_qb + 1) >> 1 : num_qb;   // workgroups per head
+  const int bh = unit / per_head;
+  int qb = unit - bh * per_head;
+  const int qb_b = qb;                // PAIR: row block B
+  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first (PAIR: A)
+  const bool has_b = PAIR && qb_b < qb;   // an odd num_qb leaves one block unpaired
 
   const HeadView hv = head_view<D>(geo, bh);
   const int N = hv.n;
@@ -442,9 +456,21 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 
   RB rb;
   rb.init(Q + head, head_bytes, lane, q0 + 32 * rg, N, c);
+  // PAIR: B's Q fragments and rows (rb takes them over at the switch), and
+  // A's rows, whose O, m and l move here at the switch.
+  RB rbb, ra;
+  if constexpr (PAIR) {
+    rbb.init(Q + head, head_bytes, lane, qb_b * ROWS + 32 * rg, N, c);
+    ra = rb;
+  }
 
   const int kv_end = CAUSAL ? min(N, q0 + ROWS) : N;
   int n_tiles = (kv_end + kBC - 1) / kBC;
+  // PAIR: A's tiles fill steps [0, jb) (tiles n_tiles .. 4 jb - 1 lie past
+  // A's diagonal); B's key tile k is pipeline tile 4 jb + k.
+  const int jb = (n_tiles + TG - 1) / TG;
+  const int n_b = has_b ? qb_b + 1 : 0;
+  const int b0 = TG * jb;
   // Split-KV: this workgroup's tiles are tb .. tb + n_tiles - 1 of the row
   // block's; K/V pointers and bounds start at tile tb, masking uses absolute
   // key positions.
@@ -461,7 +487,11 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const int kv_bytes = head_bytes - tb * TILE;
   const char* Kh = reinterpret_cast<const char*>(K + hv.kv) + (size_t)tb * TILE;
   const char* Vh = reinterpret_cast<const char*>(V + hv.kv) + (size_t)tb * TILE;
-  const int n_steps = (n_tiles + TG - 1) / TG;   // tiles per tile group
+  // Tiles per tile group.
+  const int n_steps = PAIR ? jb + (n_b + TG - 1) / TG : (n_tiles + TG - 1) / TG;
+  // Key tile of pipeline tile u, and whether it holds keys of its row block.
+  auto key_tile = [&](int u) { return (PAIR && u >= b0) ? u - b0 : u; };
+  auto tile_live = [&](int u) { return (PAIR && u >= b0) ? u - b0 < n_b : u < n_tiles; };
 
   const uint32_t lds0 = lds_addr(smem);
   // This wave's share of a tile copy in its M phase: blocks rg*LOADS .. +LOADS.
@@ -470,7 +500,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   for (int i = 0; i < LOADS; ++i) dma_offsets<D>(rg * LOADS + i, lane, koff[i], voff[i]);
   // 1 KiB block b of tile t, bounded by the range (zeros past the end).
   auto dma_tile_block = [&](bool is_v, int t, uint32_t dst, uint32_t off) {
-    dma_block_or_zero<D, FULL>(is_v ? Vh : Kh, kv_bytes, t, t < n_tiles, dst, off);
+    dma_block_or_zero<D, FULL>(is_v ? Vh : Kh, kv_bytes, key_tile(t), tile_live(t), dst, off);
   };
   auto copy_block = [&](bool is_v, int t, int i) {
     const uint32_t at = lds0 + ((is_v ? RING : 0) + t % RING) * TILE + (rg * LOADS + i) * 1024;
@@ -572,7 +602,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       wait_vmcnt<((RING - TG) / TG - 1) * 2 * LOADS>();
       return;
     }
-    rb.template mask<2>(tb + t, 0, s);
+    rb.template mask<2>(tb + key_tile(t), 0, s);
     const float m_cur = rb.m_run;
     constexpr int PAIRS = 8 * NB;
     float ex[PAIRS][2];
@@ -623,6 +653,26 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   auto mstep = [&](auto with_pv, int tq, int tv) {
     mphase(with_pv, tq, tv, tq + RING - TG, tv + RING - TG);
   };
+  // PAIR: the matrix phase that crosses from A to B (A's last PV, B's first
+  // QK) takes B's Q fragments before it; after it A's O, m and l move aside
+  // and B's rows start empty. One loop body serves both row blocks.
+  auto take_q_b = [&] {
+#pragma unroll
+    for (int k = 0; k < KSTEPS; ++k) rb.qf[k] = rbb.qf[k];
+  };
+  auto switch_rows = [&] {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      ra.o[db] = rb.o[db];
+      rb.o[db] = f32x16{};
+    }
+    ra.m_run = rb.m_run;
+    ra.l_run = rb.l_run;
+    rb.m_run = -INFINITY;
+    rb.l_run = 0.f;
+    rb.row_w = rbb.row_w;
+    rb.qrow = rbb.qrow;
+  };
   if (grp == 0) {
     rb.template qk<NB>(smem + (tile_of(0) % RING) * TILE, 0, s);
     __syncthreads();                 // its slot is refilled in phase 1
@@ -631,7 +681,12 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       sphase(tile_of(j));
       pin_p();
       __syncthreads();
+      // PAIR: step jb - 1 crosses (for an unpaired block its QK reads a tile
+      // past the end, as a last step does).
+      const bool cross = PAIR && j == jb - 1;
+      if (cross) take_q_b();
       mstep(BT{}, tile_of(j + 1), tile_of(j));
+      if (cross) switch_rows();
       __syncthreads();
     }
     __syncthreads();   // group 1's last PV
@@ -646,7 +701,11 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     pin_p();
     __syncthreads();
     for (int j = 1; j < n_steps; ++j) {
+      // PAIR: step jb crosses (if B has tiles).
+      const bool cross = PAIR && j == jb;
+      if (cross) take_q_b();
       mstep(BT{}, tile_of(j), tile_of(j - 1));
+      if (cross) switch_rows();
       __syncthreads();
       pin_s();
       sphase(tile_of(j));
@@ -660,6 +719,9 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       for (int i = 0; i < NMM; ++i) rb.o[i % DB] = mma32<BF16>(vblk_frag(vl + i * 1024), p[i / DB], rb.o[i % DB]);
     }
     __syncthreads();
+    if constexpr (PAIR) {
+      if (jb == n_steps) switch_rows();   // unpaired block: A's state in place
+    }
   }
   wait_vmem();   // copies of the last M phases
 
@@ -667,6 +729,34 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // free: all copies have landed and every read is done).
   float* area = reinterpret_cast<float*>(smem);
   __syncthreads();
+  if constexpr (PAIR) {
+    // A's records from tile groups 1 .. 3 (tile group 0 finishes A), then
+    // B's from tile groups 0, 2, 3 (tile group 1 finishes B); each
+    // finishing wave stages its O tile in its first record, once read.
+    constexpr int NREC = (TG - 1) * NRG;
+    auto rec_a = [&](int g) { return area + ((g - 1) * NRG + rg) * REC; };
+    auto rec_b = [&](int g) { return area + (NREC + (g == 0 ? 0 : g - 1) * NRG + rg) * REC; };
+    if (tg != 0) ra.save_to(rec_a(tg));
+    if (has_b && tg != 1) rb.save_to(rec_b(tg));
+    __syncthreads();
+    if (tg >= 2 || (tg == 1 && !has_b)) return;
+    // One merge and store path: tile group 0 brings A's state into rb.
+    if (tg == 0) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) rb.o[db] = ra.o[db];
+      rb.m_run = ra.m_run;
+      rb.l_run = ra.l_run;
+      rb.row_w = ra.row_w;
+      rb.qrow = ra.qrow;
+    }
+    float* r0 = tg == 0 ? rec_a(1) : rec_b(0);
+    rb.merge_from(r0);
+    rb.merge_from(tg == 0 ? rec_a(2) : rec_b(2));
+    rb.merge_from(tg == 0 ? rec_a(3) : rec_b(3));
+    static_assert(32 * RB::STAGE_STRIDE <= REC * 4, "O staging exceeds the merge record");
+    rb.template finish_staged<WRITE_L>(O + head, L + hv.l, reinterpret_cast<char*>(r0));
+    return;
+  }
   if (tg > 0) rb.save_to(area + ((tg - 1) * NRG + rg) * REC);
   __syncthreads();
   if (tg > 0) return;
@@ -685,21 +775,26 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // Kernel variants (for fa_probe_fwd_variant; the default path picks one per
 // problem shape): the ping-pong kernel with two tile groups over 128 rows and
 // a ring of 4 tiles (204), or with four tile groups over 64 rows and a ring
-// of 8 tiles (408, D = 64: twice the workgroups for the same rows).
+// of 8 tiles (408, D = 64: twice the workgroups for the same rows), or the
+// 408 kernel over pairs of causal row blocks i and num_qb - 1 - i (418).
 constexpr int kPingPong = 204;
 constexpr int kPingPong4 = 408;
+constexpr int kPairs4 = 418;
 constexpr int kGuarded = 1000;   // probe flag: force the guarded (not full-tile) instance
 
-// Query rows per workgroup, and the multiple of N that lets every tile group
-// run the same number of whole tiles (the full-tile instance).
-static int variant_rows(int variant) { return variant == kPingPong4 ? 64 : kBR; }
-static int variant_full_n(int variant) { return variant == kPingPong4 ? 256 : kBR; }
+// Query rows per row block, and the multiple of N that lets every tile group
+// run the same number of whole tiles (the full-tile instance; causal pairs
+// mask the tiles past each diagonal anyway, so whole tiles suffice).
+static int variant_rows(int variant) { return variant == kPingPong4 || variant == kPairs4 ? 64 : kBR; }
+static int variant_full_n(int variant) {
+  return variant == kPingPong4 ? 256 : variant == kPairs4 ? kBC : kBR;
+}
 
 // Variants that exist for head dimension D and the causal flag.
 static bool variant_fits(int D, int variant, int causal) {
-  (void)causal;
   if (variant == kPingPong) return true;
   if (variant == kPingPong4) return D == 64;
+  if (variant == kPairs4) return D == 64 && causal;
   return false;
 }
 
@@ -719,6 +814,13 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
     case kPingPong4:
       if constexpr (D == 64) {
         hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, false, false, 4>),
+                           dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
+        break;
+      }
+      return hipErrorInvalidValue;
+    case kPairs4:
+      if constexpr (D == 64 && CAUSAL) {
+        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, false, false, 4, true>),
                            dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
         break;
       }
@@ -752,12 +854,15 @@ constexpr int kNumCUs = 256;   // MI355X
 // short row blocks finish early and free their CUs); from 256 row blocks
 // of 128 on (non-causal) or 512 (causal) it loses (B1 H16 N2048 21.1 vs 26.5,
 // B2 H8 N4096 causal 45.1 vs 55.5), as it does for causal N = 1024 (B4 H8
-// 12.8 vs 17.6).
-static int choose_variant(int64_t D, int causal, int64_t bh, int64_t N) {
+// 12.8 vs 17.6). On that single causal wave, pairs of row blocks (418, dense
+// batches only) beat separate 64-row workgroups: B1 H8 N4096 30.3 -> 28.1,
+// B1 H16 N2048 21.1 -> 19.7 (same-process A/B); on two or more waves the
+// 128-row kernel still wins (B2 H8 N4096 47.6 vs 56.1).
+static int choose_variant(int64_t D, int causal, int64_t bh, int64_t N, bool dense) {
   if (D != 64) return kPingPong;
   const int64_t grid = bh * ((N + kBR - 1) / kBR);
   if (grid < kNumCUs) return kPingPong4;
-  if (causal && grid == kNumCUs && N >= 2048) return kPingPong4;
+  if (causal && grid == kNumCUs && N >= 2048) return dense ? kPairs4 : kPingPong4;
   return kPingPong;
 }
 
@@ -772,13 +877,16 @@ static int fwd_run(const void* q, const void* k, const void* v, void* o, float* 
   // multiple of the row block (tests compare it bitwise with the full-tile one).
   const bool guarded = variant >= kGuarded;
   if (guarded) variant -= kGuarded;
-  if (variant == 0) variant = choose_variant(D, causal, B * geo.H, geo.N);
+  if (variant == 0) variant = choose_variant(D, causal, B * geo.H, geo.N, geo.cu == nullptr);
   if (!variant_fits((int)D, variant, causal)) return FA_ERR_HEAD_DIM;
+  // Pairs need every row block of a head present (a dense batch).
+  if (variant == kPairs4 && geo.cu != nullptr) return FA_ERR_HEAD_DIM;
   const int rows = variant_rows(variant);
   const int num_qb = (geo.N + rows - 1) / rows;
   // The validation bounds the grid of 128-row blocks; 64-row blocks double it.
   if (B * geo.H * (int64_t)num_qb > (int64_t(1) << 31) - 1) return FA_ERR_TOO_LARGE;
-  const int total = (int)(B * geo.H * num_qb);
+  const int per_head = variant == kPairs4 ? (num_qb + 1) / 2 : num_qb;   // workgroups
+  const int total = (int)(B * geo.H * per_head);
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   const bool full = !guarded && geo.cu == nullptr && (geo.N % variant_full_n(variant)) == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -977,11 +1085,11 @@ extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v,
 
 extern "C" int fa_probe_default_variant(int64_t D) {
   if (D != 64 && D != 128) return 0;
-  return fa::choose_variant(D, 0, 8, 4096);
+  return fa::choose_variant(D, 0, 8, 4096, true);
 }
 
 extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal) {
-  static const int all[] = {204, 408};
+  static const int all[] = {204, 408, 418};
   int n = 0;
   for (int v : all) {
     if (fa::variant_fits((int)D, v, causal)) {

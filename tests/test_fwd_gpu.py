@@ -252,15 +252,18 @@ def test_binding_errors_on_gpu(fa, dev):
 # Every kernel variant of the forward (the default picks one per D; the others
 # stay selectable for measurement), against the oracle on ragged, causal and
 # aligned shapes, through the same C ABI with an explicit variant code.
+# Causal N = 64, 300 and 700 give an odd number of 64-row blocks (one block
+# of the paired variant 418 runs alone).
 VARIANT_CASES = [(1, 1, 64, False), (1, 2, 130, False), (1, 2, 200, False), (1, 2, 300, True),
-                 (1, 1, 384, False), (2, 3, 1000, True), (1, 2, 1024, False), (1, 1, 4095, True)]
+                 (1, 1, 384, False), (2, 3, 1000, True), (1, 2, 1024, False), (1, 1, 4095, True),
+                 (1, 1, 64, True), (1, 2, 700, True)]
 
 
 @pytest.mark.parametrize("D", [64, 128])
 def test_every_kernel_variant(fa, dev, D):
     variants = list(fa.probe.probe_fwd_variants(D, False))
     assert set(variants) == ({204, 408} if D == 64 else {204}), variants
-    assert set(fa.probe.probe_fwd_variants(D, True)) == ({204, 408} if D == 64 else {204})
+    assert set(fa.probe.probe_fwd_variants(D, True)) == ({204, 408, 418} if D == 64 else {204})
     assert fa.probe.probe_default_variant(D) in variants
     for B, H, N, causal in VARIANT_CASES:
         Q, K, V = make_fwd_inputs(B, H, N, D, seed=N + D, amp=1.0)
