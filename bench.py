@@ -1,7 +1,7 @@
 """Benchmark: FlashAttention forward TFLOP/s (and % of dense FP16 MFMA peak) at
 B=1 H=8 N=4096 D=64 on one MI355X, plus the split-KV paged decode in GB/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|widen|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|widen|copy|causal]
 
 A step is one ``forward(Q, K, V)`` call (O fp16 + L fp32) of the headline
 configuration (N=4096) on inputs resident in HBM.
@@ -305,6 +305,24 @@ def bench_sdpa(fa, torch, dev, reps=10):
     return res
 
 
+def bench_causal(fa, torch, dev, reps=7, iters=100):
+    """Causal D = 64 forward on one wave of workgroups: the default path
+    (row-block pairs, kernel variant 418) timed against the unpaired 64-row
+    kernel (variant 408, through the probe entry point) in alternating reps."""
+    res = {}
+    for (B, H, N) in ((1, 8, 4096), (1, 16, 2048)):
+        q, k, v = make_fwd(torch, dev, B, H, N, 64, seed=12)
+        f = fwd_flops(B, H, N, 64, causal=True)
+        d, u, delta = paired_delta(lambda: fa.forward(q, k, v, causal=True),
+                                   lambda: fa.probe.probe_fwd_variant(q, k, v, True, 408, True),
+                                   reps, iters, torch)
+        res[f"B{B}H{H}N{N}D64"] = {
+            "ms": round(d, 5), "TFLOPs": round(f / d / 1e9, 1),
+            "pct_peak": round(100 * f / d / 1e9 / PEAK_FP16_TFLOPS, 2),
+            "unpaired_408_ms": round(u, 5), "paired_median_delta_us": round(delta * 1000, 3)}
+    return res
+
+
 def bench_widen(fa, torch, dev, reps=5, iters=50):
     """The generality row: bf16 and GQA forward at the headline shape, and a
     packed varlen batch with the headline's total work."""
@@ -411,7 +429,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "pages", "sdpa", "widen",
-                                       "copy"],
+                                       "copy", "causal"],
                     default="all")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--burn-in", type=float, default=1.5,
@@ -435,6 +453,9 @@ def main():
         return
     if args.only == "decode":
         print(json.dumps({"decode": bench_decode(fa, torch, dev)}))
+        return
+    if args.only == "causal":
+        print(json.dumps({"causal": bench_causal(fa, torch, dev)}))
         return
     if args.only == "bwd":
         print(json.dumps({"backward": bench_backward(fa, torch, dev)}))
@@ -519,12 +540,9 @@ def main():
                 ms1 = median_of(lambda: fa.probe.probe_fwd_splitkv(q, k, v, False, 1, True),
                                 5, 10, it, torch)
                 extra[f"N{n}"].update({"splits": sp, "unsplit_ms": round(ms1, 5)})
-        q, k, v = make_fwd(torch, dev, 1, 8, 4096, 64, seed=12)
-        ms = median_of(lambda: fa.forward(q, k, v, causal=True), 5, 10, 100, torch)
-        f = fwd_flops(1, 8, 4096, 64, causal=True)
-        extra["causal_B1H8N4096D64"] = {
-            "ms": round(ms, 5), "TFLOPs": round(f / ms / 1e9, 1),
-            "pct_peak": round(100 * f / ms / 1e9 / PEAK_FP16_TFLOPS, 2)}
+        causal = bench_causal(fa, torch, dev)
+        extra["causal_B1H8N4096D64"] = causal["B1H8N4096D64"]
+        extra["causal_B1H16N2048D64"] = causal["B1H16N2048D64"]
         # a long sequence over one head: 128 row blocks for 256 CUs, so the
         # default path splits the keys in two
         q, k, v = make_fwd(torch, dev, 1, 1, 16384, 64, seed=13)

@@ -57,7 +57,9 @@ int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o, f
  * (B = 1, H = 8, N = 4096, non-causal; 0 for another D). 204 = ping-pong
  * kernel with two tile groups over 128 rows (ring of 4 tiles), 408 = with
  * four tile groups over 64 rows (ring of 8 tiles, D = 64); the forward picks
- * 408 for D = 64 where 128-row workgroups leave CUs idle. */
+ * 408 for D = 64 where 128-row workgroups leave CUs idle. 418 (causal, D = 64,
+ * dense batches only) = the 408 kernel over pairs of causal row blocks i and
+ * ceil(N/64) - 1 - i, one workgroup per pair. */
 int fa_probe_default_variant(int64_t D);
 
 /* Writes up to max_out variant codes that exist for head dimension D and the
