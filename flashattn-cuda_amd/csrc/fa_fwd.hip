@@ -798,7 +798,10 @@ static bool variant_fits(int D, int variant, int causal) {
   return false;
 }
 
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL>
+// BF16: bf16 operands (v_mfma_f32_32x32x16_bf16, P packed with
+// v_cvt_pk_bf16_f32) through the same kernels; the pointers carry 16-bit
+// elements either way.
+template <int D, bool CAUSAL, bool WRITE_L, bool FULL, bool BF16>
 static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* o,
                              float* lse, Geom geo, int num_qb, int total, float c, int variant,
                              hipStream_t stream) {
@@ -808,19 +811,19 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
   f16* Op = (f16*)o;
   switch (variant) {
     case kPingPong:
-      hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4>), dim3(total), dim3(512), 0,
-                         stream, Q, K, V, Op, lse, geo, num_qb, total, c);
+      hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4, BF16>), dim3(total),
+                         dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
       break;
     case kPingPong4:
       if constexpr (D == 64) {
-        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, false, false, 4>),
+        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, BF16, false, 4>),
                            dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
         break;
       }
       return hipErrorInvalidValue;
     case kPairs4:
       if constexpr (D == 64 && CAUSAL) {
-        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, false, false, 4, true>),
+        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, BF16, false, 4, true>),
                            dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
         break;
       }
@@ -831,16 +834,20 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool BF16>
 static hipError_t dispatch_wl(const void* q, const void* k, const void* v, void* o,
                               float* lse, Geom geo, int num_qb, int total, float c, bool full,
                               int variant, hipStream_t s) {
   if (lse) {
-    return full ? launch_fwd<D, CAUSAL, true, true>(q, k, v, o, lse, geo, num_qb, total, c, variant, s)
-                : launch_fwd<D, CAUSAL, true, false>(q, k, v, o, lse, geo, num_qb, total, c, variant, s);
+    return full ? launch_fwd<D, CAUSAL, true, true, BF16>(q, k, v, o, lse, geo, num_qb, total, c,
+                                                          variant, s)
+                : launch_fwd<D, CAUSAL, true, false, BF16>(q, k, v, o, lse, geo, num_qb, total, c,
+                                                           variant, s);
   }
-  return full ? launch_fwd<D, CAUSAL, false, true>(q, k, v, o, lse, geo, num_qb, total, c, variant, s)
-              : launch_fwd<D, CAUSAL, false, false>(q, k, v, o, lse, geo, num_qb, total, c, variant, s);
+  return full ? launch_fwd<D, CAUSAL, false, true, BF16>(q, k, v, o, lse, geo, num_qb, total, c,
+                                                         variant, s)
+              : launch_fwd<D, CAUSAL, false, false, BF16>(q, k, v, o, lse, geo, num_qb, total, c,
+                                                          variant, s);
 }
 
 constexpr int kNumCUs = 256;   // MI355X
@@ -872,7 +879,8 @@ namespace fa {
 // The forward over a head geometry with an explicit kernel variant (0: the
 // default choice). Arguments are already validated.
 static int fwd_run(const void* q, const void* k, const void* v, void* o, float* lse,
-                   const Geom& geo, int64_t B, int64_t D, int causal, int variant, void* stream) {
+                   const Geom& geo, int64_t B, int64_t D, int causal, int variant, void* stream,
+                   bool bf16 = false) {
   // kGuarded + v: variant v through its guarded instance even where N is a
   // multiple of the row block (tests compare it bitwise with the full-tile one).
   const bool guarded = variant >= kGuarded;
@@ -891,13 +899,16 @@ static int fwd_run(const void* q, const void* k, const void* v, void* o, float* 
   const bool full = !guarded && geo.cu == nullptr && (geo.N % variant_full_n(variant)) == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
+#define FA_FWD_DISPATCH(DD, CC, BB) \
+  dispatch_wl<DD, CC, BB>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s)
   if (D == 64) {
-    e = causal ? dispatch_wl<64, true>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s)
-               : dispatch_wl<64, false>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s);
+    if (bf16) e = causal ? FA_FWD_DISPATCH(64, true, true) : FA_FWD_DISPATCH(64, false, true);
+    else e = causal ? FA_FWD_DISPATCH(64, true, false) : FA_FWD_DISPATCH(64, false, false);
   } else {
-    e = causal ? dispatch_wl<128, true>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s)
-               : dispatch_wl<128, false>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s);
+    if (bf16) e = causal ? FA_FWD_DISPATCH(128, true, true) : FA_FWD_DISPATCH(128, false, true);
+    else e = causal ? FA_FWD_DISPATCH(128, true, false) : FA_FWD_DISPATCH(128, false, false);
   }
+#undef FA_FWD_DISPATCH
   return e == hipSuccess ? FA_OK : -(int)e;
 }
 
@@ -1024,34 +1035,6 @@ extern "C" int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, vo
   return fa::fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream);
 }
 
-namespace fa {
-// bfloat16 forward: the default (ping-pong) kernel with bf16 operands
-// (v_mfma_f32_32x32x16_bf16, P packed with v_cvt_pk_bf16_f32).
-template <int D, bool CAUSAL, bool WRITE_L, bool FULL>
-static void launch_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
-                        const Geom& geo, int num_qb, int total, float c, hipStream_t s) {
-  const f16* Q = (const f16*)q;
-  const f16* K = (const f16*)k;
-  const f16* V = (const f16*)v;
-  f16* O = (f16*)o;
-  hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 4, true>), dim3(total), dim3(512), 0,
-                     s, Q, K, V, O, lse, geo, num_qb, total, c);
-}
-
-template <int D, bool CAUSAL>
-static void dispatch_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
-                          const Geom& geo, int num_qb, int total, float c, bool full,
-                          hipStream_t s) {
-  if (lse) {
-    if (full) launch_bf16<D, CAUSAL, true, true>(q, k, v, o, lse, geo, num_qb, total, c, s);
-    else launch_bf16<D, CAUSAL, true, false>(q, k, v, o, lse, geo, num_qb, total, c, s);
-  } else {
-    if (full) launch_bf16<D, CAUSAL, false, true>(q, k, v, o, lse, geo, num_qb, total, c, s);
-    else launch_bf16<D, CAUSAL, false, false>(q, k, v, o, lse, geo, num_qb, total, c, s);
-  }
-}
-}  // namespace fa
-
 extern "C" int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                            int64_t B, int64_t H, int64_t H_kv, int64_t N, int64_t D, int causal,
                            void* stream) {
@@ -1060,20 +1043,8 @@ extern "C" int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o,
   if (st != FA_OK) return st;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
   const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
-  const int num_qb = (int)((N + kBR - 1) / kBR);
-  const int total = (int)(B * H * num_qb);
-  const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
-  const bool full = (N % kBR) == 0;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (D == 64) {
-    if (causal) dispatch_bf16<64, true>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
-    else dispatch_bf16<64, false>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
-  } else {
-    if (causal) dispatch_bf16<128, true>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
-    else dispatch_bf16<128, false>(q, k, v, o, lse, geo, num_qb, total, c, full, s);
-  }
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? FA_OK : -(int)e;
+  // The fp16 path's kernel choice for the shape, with bf16 operands.
+  return fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream, true);
 }
 
 extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o,

@@ -1,4 +1,7 @@
-"""GPU tier: the bfloat16 paths against the CPU oracle: forward (forward_bf16),
+"""GPU tier: the bfloat16 paths against the CPU oracle: forward (forward_bf16,
+which picks its kernel from the shape as the fp16 forward does: the D = 64
+cases run the 64-row kernel, the 128-row one at N = 4096 and, causal there,
+the row-block pairs),
 backward (backward_bf16), paged decode and page writer (decode_paged and
 kv_append with bf16 tensors).
 
@@ -30,7 +33,7 @@ def bf16_half_ulp(x):
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("B,H,Hkv,N,causal", [
     (1, 1, 1, 1, False), (1, 2, 2, 63, True), (2, 4, 4, 256, False), (1, 8, 2, 1000, True),
-    (1, 8, 8, 4096, False),
+    (1, 8, 8, 4096, False), (1, 8, 8, 4096, True),
 ])
 def test_bf16_forward(fa, dev, D, B, H, Hkv, N, causal):
     rng = np.random.default_rng(N + D + H)
