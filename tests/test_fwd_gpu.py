@@ -120,6 +120,21 @@ def test_config2_headline(fa, dev, N):
     _run_case(fa, dev, 1, 8, N, 64, dtype=torch.float16, strict=True)
 
 
+@pytest.mark.parametrize("H,N", [(8, 4096), (16, 2048)])
+def test_causal_single_wave_row_block_pairs(fa, dev, H, N):
+    """Causal D64 on exactly 256 row blocks of 128 rows: the default path runs
+    the row-block pairs (kernel variant 418); against the oracle, and the
+    same bits on a repeat launch."""
+    _run_case(fa, dev, 1, H, N, 64, causal=True, dtype=torch.float16, strict=True)
+    Q, K, V = make_fwd_inputs(1, H, N, 64, seed=7)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O0, L0 = fa.forward(tq, tk, tv, causal=True)
+    Op, Lp = fa.probe.probe_fwd_variant(tq, tk, tv, True, 418, True)
+    O1, L1 = fa.forward(tq, tk, tv, causal=True)
+    assert torch.equal(O0, Op) and torch.equal(L0, Lp), "default path is variant 418"
+    assert torch.equal(O0, O1) and torch.equal(L0, L1)
+
+
 def test_config2_n8192_sampled_heads(fa, dev):
     """N=8192: full GPU run, oracle on two heads."""
     B, H, N, D = 1, 8, 8192, 64

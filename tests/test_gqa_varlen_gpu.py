@@ -41,6 +41,24 @@ def test_gqa_forward(fa, dev, D, Hkv, N, causal):
     _check(O, L, Or, Lr, tag=f"GQA H{H} Hkv{Hkv} N{N} D{D} causal={causal}")
 
 
+@pytest.mark.parametrize("Hkv", [4, 1])
+def test_gqa_causal_row_block_pairs(fa, dev, Hkv):
+    """B1 H16 N2048 D64 causal: the default path runs the row-block pairs
+    (one workgroup per pair of 64-row blocks i and 31 - i), here with K/V
+    heads shared by groups of query heads."""
+    B, H, N, D = 1, 16, 2048, 64
+    Q = _randn((B, H, N, D), 11)
+    K = _randn((B, Hkv, N, D), 12)
+    V = _randn((B, Hkv, N, D), 13)
+    tq, tk, tv = (torch.from_numpy(x).to(dev) for x in (Q, K, V))
+    O, L = fa.forward(tq, tk, tv, causal=True)
+    torch.cuda.synchronize()
+    g = H // Hkv
+    Or, Lr = naive_attention(half_cast(Q), np.repeat(half_cast(K), g, axis=1),
+                             np.repeat(half_cast(V), g, axis=1), causal=True)
+    _check(O, L, Or, Lr, tag=f"GQA pairs H{H} Hkv{Hkv} N{N} D{D} causal")
+
+
 def test_gqa_with_all_heads_equals_mha(fa, dev):
     Q, K, V = (_randn((1, 4, 300, 64), s) for s in (4, 5, 6))
     tq, tk, tv = (torch.from_numpy(x).to(dev).half() for x in (Q, K, V))
