@@ -230,6 +230,126 @@ struct RowBlock {
     }
   }
 
+  // Parallel merge of the TG tile groups holding partial (m, l, O) for the
+  // same rows: tile group P finishes part P of the O registers (groups
+  // P·PG .. P·PG + PG − 1 of four registers, i.e. 16-byte chunks 2·P·PG/2 ..
+  // of every row), so the TG waves merge and store at once instead of one
+  // wave merging TG − 1 records. A part record holds m and l of the 64 lanes
+  // and, lane-major like the full record, the parts of the other tile groups
+  // (part p at slot p − (p > owner)).
+  template <int TG>
+  static constexpr int part_groups() { return 4 * DB / TG; }
+  template <int TG>
+  static constexpr int part_rec_floats() { return (2 + (TG - 1) * part_groups<TG>() * 4) * 64; }
+  template <int TG>
+  __device__ __forceinline__ static int part_off(int slot, int gi, int lane) {
+    return 128 + ((slot * part_groups<TG>() + gi) * 64 + lane) * 4;
+  }
+
+  template <int TG>
+  __device__ __forceinline__ void save_parts(float* rec, int self) const {
+    constexpr int PG = part_groups<TG>();
+    rec[lane] = m_run;
+    rec[64 + lane] = l_run;
+    static_for<0, TG>([&](auto pi) {
+      constexpr int p = decltype(pi)::value;
+      if (p != self) {
+        const int slot = p - (p > self ? 1 : 0);
+#pragma unroll
+        for (int gi = 0; gi < PG; ++gi) {
+          const int g = p * PG + gi;
+          *reinterpret_cast<f32x4*>(rec + part_off<TG>(slot, gi, lane)) =
+              f32x4{o[g / 4][4 * (g % 4)], o[g / 4][4 * (g % 4) + 1], o[g / 4][4 * (g % 4) + 2],
+                    o[g / 4][4 * (g % 4) + 3]};
+        }
+      }
+    });
+  }
+
+  // This wave's part P of the merged, normalised O tile into the row group's
+  // `stage` (32 rows of STAGE_STRIDE bytes, shared by the TG waves); rec(i)
+  // is tile group i's part record. Leaves the merged m and l in m_run, l_run
+  // (every part computes the same values, in the same order).
+  template <int TG, int P, typename Rec>
+  __device__ __forceinline__ void merge_part_stage(Rec rec, char* stage) {
+    constexpr int PG = part_groups<TG>();
+    float mi[TG], li[TG];
+#pragma unroll
+    for (int i = 0; i < TG; ++i) {
+      mi[i] = i == P ? m_run : rec(i)[lane];
+      li[i] = i == P ? l_run : rec(i)[64 + lane];
+    }
+    float M = mi[0];
+#pragma unroll
+    for (int i = 1; i < TG; ++i) M = fmaxf(M, mi[i]);
+    float a[TG];
+    float l = 0.f;
+#pragma unroll
+    for (int i = 0; i < TG; ++i) {
+      a[i] = (mi[i] == M) ? 1.f : exp2_hw(mi[i] - M);
+      l += li[i] * a[i];
+    }
+    f32x4 acc[PG];
+#pragma unroll
+    for (int gi = 0; gi < PG; ++gi) {
+      const int g = P * PG + gi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[gi][e] = o[g / 4][4 * (g % 4) + e] * a[P];
+    }
+#pragma unroll
+    for (int i = 0; i < TG; ++i) {
+      if (i == P) continue;
+      const int slot = P - (P > i ? 1 : 0);
+#pragma unroll
+      for (int gi = 0; gi < PG; ++gi) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(rec(i) + part_off<TG>(slot, gi, lane));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[gi][e] = fmaf(v[e], a[i], acc[gi][e]);
+      }
+    }
+    m_run = M;
+    l_run = l;
+    const float inv = 1.f / sum_xor32(l);
+#pragma unroll
+    for (int gi = 0; gi < PG; gi += 2) {
+      const int g = P * PG + gi;                     // even: a pair of groups
+      uint32_t w[2][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f16x2 x0 = cvt2x<BF16>(acc[gi + j][0] * inv, acc[gi + j][1] * inv);
+        const f16x2 x1 = cvt2x<BF16>(acc[gi + j][2] * inv, acc[gi + j][3] * inv);
+        w[j][0] = __builtin_bit_cast(uint32_t, x0);
+        w[j][1] = __builtin_bit_cast(uint32_t, x1);
+      }
+      const auto r0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
+      const auto r1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
+      const int chunk = 4 * (g / 4) + 2 * ((g % 4) / 2) + hi;   // 16-byte chunk of the row
+      *reinterpret_cast<uint4*>(stage + (lane & 31) * STAGE_STRIDE + chunk * 16) =
+          uint4{r0[0], r1[0], r0[1], r1[1]};
+    }
+  }
+
+  // After every part is staged (a barrier): wave `self` of the TG stores its
+  // share of the row group's 16-byte chunks, and tile group 0 writes L.
+  template <int TG, bool WRITE_L>
+  __device__ __forceinline__ void store_staged_part(f16* Oh, float* Lh, const char* stage,
+                                                    int self) const {
+    constexpr int CPR = D / 8;
+    constexpr int PER = 32 * CPR / (64 * TG);
+    static_assert(PER * 64 * TG == 32 * CPR, "whole chunks per lane");
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int idx = (k * TG + self) * 64 + lane;
+      const int r = idx / CPR, ch = idx % CPR;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * STAGE_STRIDE + ch * 16);
+      if (FULL || row_w + r < N)
+        *reinterpret_cast<uint4*>(Oh + (size_t)(row_w + r) * D + ch * 8) = v;
+    }
+    const float l_tot = sum_xor32(l_run);   // all lanes: a cross-lane exchange
+    if (WRITE_L && self == 0 && hi == 0 && (FULL || qrow < N))
+      Lh[qrow] = (m_run + log2_hw(l_tot)) * kLn2;
+  }
+
   // Combine the two half-rows, normalise and store O (and L), staged through
   // this wave's `stage` LDS area (at least 32 rows of STAGE_STRIDE bytes,
   // written and read only by this wave):
@@ -423,7 +543,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int NMM = NB * KSTEPS;             // MFMAs of one QK (= of one PV)
   constexpr int PF = D == 64 ? 8 : 4;          // operand prefetch distance, in MFMAs
   constexpr int REC = RB::REC_FLOATS;          // floats per wave record of the merge
-  static_assert((PAIR ? 2 : 1) * (TG - 1) * NRG * REC * 4 <= 2 * RING * TILE, "merge area too small");
+  static_assert(!SPLITKV || (TG - 1) * NRG * REC * 4 <= 2 * RING * TILE, "merge area too small");
   // K slots at [0, RING) * TILE, V slots at [RING, 2 RING) * TILE.
   __shared__ __attribute__((aligned(1024))) char smem[2 * RING * TILE];
 
@@ -725,15 +845,24 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   }
   wait_vmem();   // copies of the last M phases
 
-  // Merge tile groups 1 .. TG-1 into tile group 0 through LDS (the ring is
-  // free: all copies have landed and every read is done).
+  // Merge the tile groups' partial rows through LDS (the ring is free: all
+  // copies have landed and every read is done).
   float* area = reinterpret_cast<float*>(smem);
   __syncthreads();
+  // Every tile group merges and stores one part of the O columns of its
+  // rows (RowBlock::merge_part_stage), through part records and a staging
+  // tile per row group after them.
+  constexpr int PREC = RB::template part_rec_floats<TG>();
+  constexpr int RECS = TG * NRG * PREC;                 // floats of one row block's records
+  constexpr int STAGE_BYTES = NRG * 32 * RB::STAGE_STRIDE;
   if constexpr (PAIR) {
-    // A's records from tile groups 1 .. 3 (tile group 0 finishes A), then
-    // B's from tile groups 0, 2, 3 (tile group 1 finishes B); each
-    // finishing wave stages its O tile in its first record, once read.
+    // Tile group 0 merges A's rows from the records of groups 1 .. 3 and
+    // tile group 1 B's from groups 0, 2, 3, in parallel, with full records
+    // (the part merge above measured slower here: four waves in two passes,
+    // or 236 VGPRs with one merge instance per row block); each finishing
+    // wave stages its O tile in its first record, once read.
     constexpr int NREC = (TG - 1) * NRG;
+    static_assert(2 * NREC * REC * 4 <= 2 * RING * TILE, "merge area too small");
     auto rec_a = [&](int g) { return area + ((g - 1) * NRG + rg) * REC; };
     auto rec_b = [&](int g) { return area + (NREC + (g == 0 ? 0 : g - 1) * NRG + rg) * REC; };
     if (tg != 0) ra.save_to(rec_a(tg));
@@ -757,19 +886,28 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     rb.template finish_staged<WRITE_L>(O + head, L + hv.l, reinterpret_cast<char*>(r0));
     return;
   }
+  if constexpr (!SPLITKV) {
+    static_assert(RECS * 4 + STAGE_BYTES <= 2 * RING * TILE, "merge area too small");
+    auto rec = [&](int i) { return area + (i * NRG + rg) * PREC; };
+    char* stage = reinterpret_cast<char*>(area + RECS) + rg * 32 * RB::STAGE_STRIDE;
+    rb.template save_parts<TG>(rec(tg), tg);
+    __syncthreads();
+    static_for<0, TG>([&](auto pi) {
+      constexpr int P = decltype(pi)::value;
+      if (tg == P) rb.template merge_part_stage<TG, P>(rec, stage);
+    });
+    __syncthreads();
+    rb.template store_staged_part<TG, WRITE_L>(O + head, L + hv.l, stage, tg);
+    return;
+  }
+  // Split-KV: tile group 0 merges the others' records and writes the fp32
+  // partial.
   if (tg > 0) rb.save_to(area + ((tg - 1) * NRG + rg) * REC);
   __syncthreads();
   if (tg > 0) return;
 #pragma unroll
   for (int g = 1; g < TG; ++g) rb.merge_from(area + ((g - 1) * NRG + rg) * REC);
-  area += rg * REC;   // this wave's first record, read: it stages the O tile
-  if constexpr (SPLITKV) {
-    rb.finish_partial(part_o, part_lse, (hv.l + rb.qrow) * nsplit + split);
-  } else {
-    // this wave's merge record is read; its area stages the O tile
-    static_assert(32 * RB::STAGE_STRIDE <= REC * 4, "O staging exceeds the merge record");
-    rb.template finish_staged<WRITE_L>(O + head, L + hv.l, reinterpret_cast<char*>(area));
-  }
+  rb.finish_partial(part_o, part_lse, (hv.l + rb.qrow) * nsplit + split);
 }
 
 // Kernel variants (for fa_probe_fwd_variant; the default path picks one per
