@@ -267,11 +267,12 @@ def test_binding_errors_on_gpu(fa, dev):
 # Every kernel variant of the forward (the default picks one per D; the others
 # stay selectable for measurement), against the oracle on ragged, causal and
 # aligned shapes, through the same C ABI with an explicit variant code.
-# Causal N = 64, 300 and 700 give an odd number of 64-row blocks (one block
-# of the paired variant 418 runs alone).
+# Causal N = 64, 300, 320 and 700 give an odd number of 64-row blocks (one
+# block of the paired variant 418 runs alone; at N = 320 in its full-tile
+# instance).
 VARIANT_CASES = [(1, 1, 64, False), (1, 2, 130, False), (1, 2, 200, False), (1, 2, 300, True),
                  (1, 1, 384, False), (2, 3, 1000, True), (1, 2, 1024, False), (1, 1, 4095, True),
-                 (1, 1, 64, True), (1, 2, 700, True)]
+                 (1, 1, 64, True), (1, 2, 700, True), (1, 2, 320, True)]
 
 
 @pytest.mark.parametrize("D", [64, 128])
@@ -299,7 +300,8 @@ def test_every_kernel_variant(fa, dev, D):
 # paths, tests/test_fa3_db_full.py:47, :58-66).
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("B,H,N", [(1, 2, 128), (2, 3, 512), (1, 2, 1024), (1, 1, 4096)])
+@pytest.mark.parametrize("B,H,N", [(1, 2, 128), (2, 3, 512), (1, 2, 1024), (1, 1, 4096),
+                                   (1, 2, 320)])
 def test_full_tiles_match_guarded_bitwise(fa, dev, D, causal, B, H, N):
     Q, K, V = make_fwd_inputs(B, H, N, D, seed=N + D + int(causal), amp=1.0)
     tq, tk, tv = _to_dev(dev, Q, K, V)
