@@ -293,6 +293,21 @@ def test_every_kernel_variant(fa, dev, D):
             _check(O, L, Or, Lr, 1.0, tag=f"variant {v} B{B} H{H} N{N} D{D} causal={causal}")
 
 
+# The row-block pairs (418) on ragged and small causal shapes: one block
+# unpaired (odd block counts), A's tiles rounded up past its diagonal, and
+# B's first tile as the wave's first after the switch.
+@pytest.mark.parametrize("N", [1, 63, 65, 127, 129, 191, 257, 383, 449, 577, 1023, 1089])
+def test_row_block_pairs_ragged_causal(fa, dev, N):
+    Q, K, V = make_fwd_inputs(1, 2, N, 64, seed=1000 + N, amp=1.0)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O, L = fa.probe.probe_fwd_variant(tq, tk, tv, True, 418, True)
+    (O2,) = fa.probe.probe_fwd_variant(tq, tk, tv, True, 418, False)
+    torch.cuda.synchronize()
+    assert torch.equal(O, O2), "O-only differs"
+    Or, Lr = naive_attention(half_cast(Q), half_cast(K), half_cast(V), causal=True)
+    _check(O, L, Or, Lr, 1.0, tag=f"pairs N{N}", strict=True)
+
+
 # The full-tile instance (no bounds predicates, chosen when N is a multiple of
 # the 128-row block) against the guarded one forced through the probe on the
 # same aligned shapes: the predicates only ever remove keys or rows past N, so
