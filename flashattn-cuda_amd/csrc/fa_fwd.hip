@@ -8,9 +8,11 @@
 // (cuda/flash_attn_fa3_db_full.cu:202, :250-284, :319-343).
 //
 // Work decomposition (CDNA4):
-//   * a workgroup owns 128 query rows of one (b, h), 8 waves; a 1-D grid with
-//     an XCD-aware remap keeps the query blocks of a head on one XCD so its
-//     K/V stay in that XCD's L2;
+//   * a workgroup owns 128 query rows of one (b, h), 8 waves (64 rows with
+//     four key-tile groups where 128-row blocks leave CUs idle, and causal
+//     row blocks i and num_qb - 1 - i together on a single wave of
+//     workgroups); a 1-D grid with an XCD-aware remap keeps the query blocks
+//     of a head on one XCD so its K/V stay in that XCD's L2;
 //   * K/V advance in 64-key tiles, copied global -> LDS by buffer_load ... lds
 //     into rings of LDS slots while earlier tiles are consumed; every LDS
 //     operand read has a constant offset from a per-lane base;
@@ -24,7 +26,8 @@
 // alternate, barrier by barrier, between a matrix phase and a softmax phase,
 // so each SIMD runs one wave's MFMAs while the other wave's VALU work issues.
 // Template flags: D in {64,128}, CAUSAL, WRITE_L (O-only when false), FULL
-// (N % 128 == 0: no bounds predicates).
+// (N a multiple of the variant's full-tile unit: no bounds predicates), BF16,
+// SPLITKV, TG (key-tile groups), PAIR (causal row-block pairs).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
