@@ -1,7 +1,7 @@
 """Benchmark: FlashAttention forward TFLOP/s (and % of dense FP16 MFMA peak) at
 B=1 H=8 N=4096 D=64 on one MI355X, plus the split-KV paged decode in GB/s.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|widen|copy|causal]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|bwd|decode|pages|sdpa|widen|copy|causal|readbw]
 
 A step is one ``forward(Q, K, V)`` call (O fp16 + L fp32) of the headline
 configuration (N=4096) on inputs resident in HBM.
@@ -141,6 +141,24 @@ def decode_meta(B=32, ctx_lo=512, ctx_hi=32768, page_size=16, seed=5):
         table[b, :pages[b]] = perm[off:off + pages[b]]
         off += pages[b]
     return ctx, table, num_pages
+
+
+def bench_read_ceiling(fa, torch, dev, reps=5, iters=5):
+    """HBM read rate of a plain streaming kernel (fa_probe_read_bw: 16-byte
+    loads, 8 in flight per thread) over 4 GiB, at several grid sizes: the
+    practical ceiling the decode's split pass is compared with."""
+    nbytes = 4 * 1024 ** 3
+    x = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    res = {}
+    for blocks in (4096, 8192, 16384):
+        ms = median_of(lambda: fa.probe.probe_read_bw(x, sink, blocks), reps, 2, iters, torch)
+        res[f"blocks_{blocks}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    del x
+    torch.cuda.empty_cache()
+    res["best_GBps"] = max(v for k, v in res.items())
+    res["bytes"] = nbytes
+    return res
 
 
 def bench_decode(fa, torch, dev, reps=5, iters=20):
@@ -429,7 +447,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["all", "fwd", "bwd", "decode", "pages", "sdpa", "widen",
-                                       "copy", "causal"],
+                                       "copy", "causal", "readbw"],
                     default="all")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--burn-in", type=float, default=1.5,
@@ -456,6 +474,9 @@ def main():
         return
     if args.only == "causal":
         print(json.dumps({"causal": bench_causal(fa, torch, dev)}))
+        return
+    if args.only == "readbw":
+        print(json.dumps({"read_ceiling": bench_read_ceiling(fa, torch, dev)}))
         return
     if args.only == "bwd":
         print(json.dumps({"backward": bench_backward(fa, torch, dev)}))
@@ -566,6 +587,7 @@ def main():
         del q, k, v
         out["extra"] = extra
         out["decode"] = bench_decode(fa, torch, dev)
+        out["read_ceiling"] = bench_read_ceiling(fa, torch, dev)
         out["backward"] = bench_backward(fa, torch, dev)
         out["kv_append"] = bench_pages(fa, torch, dev)
         out["sdpa_comparator"] = bench_sdpa(fa, torch, dev)

@@ -60,6 +60,7 @@ SIGNATURES = {
     "fa_probe_fwd_variant": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp]),
     "fa_probe_fwd_variants": (C.c_int, [_vp, C.c_int, _i64, C.c_int]),
     "fa_probe_default_variant": (C.c_int, [_i64]),
+    "fa_probe_read_bw": (C.c_int, [_vp, _i64, C.c_int, _vp, _vp]),
 }
 
 DECODE_SCRATCH_FLOATS = 1 << 22   # FA_DECODE_SCRATCH_FLOATS

@@ -196,3 +196,37 @@ extern "C" int fa_probe_chain(const void* q, const void* k, const void* v, float
   }
   return finish();
 }
+
+namespace fa {
+// Streaming read of `n` 16-byte vectors, grid-stride with 8 loads in flight
+// per thread, folded into one word per lane (written only on a 2^-32
+// chance, so the loads stay and the stores do not count): the HBM read rate
+// a plain kernel reaches, the ceiling the paged decode is compared with.
+__global__ void __launch_bounds__(256)
+probe_read_kernel(const uint4* __restrict__ p, size_t n, uint32_t* __restrict__ sink) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * 256;
+  uint32_t acc = 0;
+  for (; i + 7 * stride < n; i += 8 * stride) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < n; i += stride) {
+    const uint4 v = p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+}  // namespace fa
+
+extern "C" int fa_probe_read_bw(const void* p, int64_t bytes, int blocks, uint32_t* sink,
+                                void* stream) {
+  if (!p || !sink) return 1;
+  if (bytes < 16 || (bytes & 15) || blocks < 1 || (reinterpret_cast<uintptr_t>(p) & 15u)) return 2;
+  hipLaunchKernelGGL(fa::probe_read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint4*)p, (size_t)(bytes / 16), sink);
+  return finish();
+}

@@ -519,6 +519,18 @@ std::vector<torch::Tensor> probe_frags(torch::Tensor tile) {
   return {kout, vout};
 }
 
+// One streaming read of x (any dtype, contiguous, 16-byte multiple) into the
+// one-word sink (int32, CUDA): the read-bandwidth probe.
+void probe_read_bw(torch::Tensor x, torch::Tensor sink, int64_t blocks) {
+  TORCH_CHECK(x.is_cuda() && x.is_contiguous(), "x must be a contiguous CUDA tensor");
+  TORCH_CHECK(sink.is_cuda() && sink.scalar_type() == torch::kInt && sink.numel() >= 1,
+              "sink must be a CUDA int32 tensor");
+  const int64_t bytes = x.numel() * (int64_t)x.element_size();
+  check_status(fa_probe_read_bw(x.data_ptr(), bytes, (int)blocks,
+                                reinterpret_cast<uint32_t*>(sink.data_ptr<int>()), current_stream(x)),
+               "fa_probe_read_bw");
+}
+
 torch::Tensor probe_chain(torch::Tensor q, torch::Tensor k, torch::Tensor v) {
   TORCH_CHECK(q.is_cuda() && q.dim() == 2 && q.size(0) == 32 && q.scalar_type() == torch::kHalf);
   const int64_t D = q.size(1);
@@ -572,6 +584,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("probe_permlane", &probe_permlane);
   m.def("probe_frags", &probe_frags);
   m.def("probe_chain", &probe_chain);
+  m.def("probe_read_bw", &probe_read_bw, py::arg("x"), py::arg("sink"), py::arg("blocks"));
   m.def("probe_fwd_variant", &probe_fwd_variant, py::arg("Q"), py::arg("K"), py::arg("V"),
         py::arg("causal") = false, py::arg("variant") = 12, py::arg("want_L") = true);
   m.def("probe_fwd_variants", &probe_fwd_variants);

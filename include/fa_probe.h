@@ -66,6 +66,14 @@ int fa_probe_default_variant(int64_t D);
  * causal flag into out (may be NULL) and returns how many there are. */
 int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal);
 
+/* Streams `bytes` (a multiple of 16, 16-byte aligned) from device memory at p
+ * with `blocks` workgroups of 256 threads, 16-byte loads, 8 in flight per
+ * thread: the read bandwidth a plain kernel reaches on this device, the
+ * ceiling the paged decode's split pass is measured against. sink: one
+ * device uint32, written only on a 2^-32 chance. 1: NULL argument, 2: bad
+ * size, alignment or grid. */
+int fa_probe_read_bw(const void* p, int64_t bytes, int blocks, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -307,3 +307,14 @@ def test_bf16_decode_and_page_writer_reject_before_touching_the_device(capi):
     assert lib.fa_decode_paged_bf16(*gqa) == capi.STATUS["FA_ERR_NULL_POINTER"]
     assert lib.fa_kv_append_bf16(*_kv(ps=8), None) == capi.STATUS["FA_ERR_PAGE_SIZE"]
     assert lib.fa_kv_append_bf16(*_kv(T=0), None) == capi.STATUS["FA_OK"]   # no launch
+
+
+def test_read_probe_rejects_before_touching_the_device(capi):
+    """fa_probe_read_bw checks its pointers, size, alignment and grid first."""
+    lib = capi.load()
+    assert lib.fa_probe_read_bw(None, 1024, 8, A, None) == 1
+    assert lib.fa_probe_read_bw(A, 1024, 8, None, None) == 1
+    assert lib.fa_probe_read_bw(A, 1000, 8, A, None) == 2     # not a multiple of 16
+    assert lib.fa_probe_read_bw(A, 0, 8, A, None) == 2
+    assert lib.fa_probe_read_bw(A, 1024, 0, A, None) == 2     # no workgroups
+    assert lib.fa_probe_read_bw(A + 8, 1024, 8, A, None) == 2  # 8-byte aligned only

@@ -90,3 +90,14 @@ def test_qk_pv_chain(fa, dev, D):
     perm = torch.arange(64).view(4, 16).flip(1).reshape(-1)
     bad = s.half().float() @ v.float().cpu()[perm]
     assert (got - bad).abs().max().item() > 0.1
+
+
+def test_read_bandwidth_probe_runs(fa, dev):
+    """The read-bandwidth probe streams a buffer without writing the sink
+    (all-zero input folds to 0, not the sink's trigger value)."""
+    x = torch.zeros(16 << 20, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for blocks in (1, 64, 4096):
+        fa.probe.probe_read_bw(x, sink, blocks)
+    torch.cuda.synchronize()
+    assert sink.item() == 0
