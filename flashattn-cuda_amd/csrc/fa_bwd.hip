@@ -544,9 +544,10 @@ __device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __
 // and sync each group's four waves on their copies. Tile j's stage is read
 // from S(j - 1), which loads tile j's A operands into registers (M(j) then
 // issues its score products without LDS waits), to M(j + 1), which reads its
-// C operands. S(j) starts the copies of tile j + 2 into the stage of tile
-// j - 2 (last read in M(j - 1)) and M(j + 1) waits for them: a ring of 4
-// stages, with the copy issue in the VALU phase.
+// C operands. S(j) starts the copies of tile j + 3 into the stage of tile
+// j - 1 (last read in M(j), before the barrier that starts S(j)) and M(j + 2)
+// waits for them, leaving those of S(j + 1) in flight: a ring of 4 stages,
+// with the copy issue in the VALU phase.
 // ---------------------------------------------------------------------------
 constexpr int kPPStages = 4;
 
@@ -634,9 +635,18 @@ __device__ __forceinline__ void dkdv_body_pp(const f16* __restrict__ Q, const f1
     if (kw == 0) copy_rowvec(Lh, N, t, base + 4 * TILE + 512 * grp, lane);
     if (kw == 1) copy_rowvec(Dh, N, t, base + 4 * TILE + 512 * grp + 256, lane);
   };
+  // Copies run three tiles ahead: at the end of M phase j tile j + 1 must
+  // have landed, and tile j + 2's copies (this wave's last issue) may still
+  // be in flight.
+  auto wait_next = [&](bool later_in_flight) {
+    if (!later_in_flight) wait_vmem();
+    else if (kw < 2) wait_vmcnt<OWN + 1>();
+    else wait_vmcnt<OWN>();
+  };
   issue_own(t0, 0);
   if (T > 1) issue_own(t0 + 1, 1);
-  wait_vmem();
+  if (T > 2) issue_own(t0 + 2, 2);
+  wait_next(T > 2);
   __syncthreads();
 
   f32x16 s = {}, dp = {};   // this wave's scores of its current tile
@@ -687,12 +697,13 @@ __device__ __forceinline__ void dkdv_body_pp(const f16* __restrict__ Q, const f1
       if constexpr (WC) mma_c(cf[kk], kk);
       __builtin_amdgcn_sched_barrier(0);   // keep every product in this phase
     });
-    wait_vmem();
+    wait_next(j + 2 < T);
   };
-  // S phase of relative tile j: the copies of tile j + 2, P and dS into pb,
-  // gb, and tile j + 1's A operands.
+  // S phase of relative tile j: the copies of tile j + 3 (into the stage of
+  // tile j - 1, whose last reads were this group's M phase j), P and dS into
+  // pb, gb, and tile j + 1's A operands.
   auto sphase = [&](int j) {
-    if (j + 2 < T) issue_own(t0 + j + 2, (j + 2) % kPPStages);
+    if (j + 3 < T) issue_own(t0 + j + 3, (j + 3) % kPPStages);
     const char* sb = stage_of(j);
     const int qt0 = (t0 + j) * kBQ;
     const float* ls = reinterpret_cast<const float*>(sb + 4 * TILE + 512 * grp);
@@ -830,9 +841,15 @@ __device__ __forceinline__ void dq_body_pp(const f16* __restrict__ Q, const f16*
                     part == 1 ? vo : ko);
     }
   };
+  // Copies run three tiles ahead (as in the dK/dV body).
+  auto wait_next = [&](bool later_in_flight) {
+    if (later_in_flight) wait_vmcnt<PER>();
+    else wait_vmem();
+  };
   issue_own(0, 0);
   if (T > 1) issue_own(1, 1);
-  wait_vmem();
+  if (T > 2) issue_own(2, 2);
+  wait_next(T > 2);
   __syncthreads();
 
   f32x16 s = {}, dp = {};
@@ -871,10 +888,10 @@ __device__ __forceinline__ void dq_body_pp(const f16* __restrict__ Q, const f16*
       if constexpr (WC) acc[0][kk % DB] = mma32<BF16>(cf[kk], gb[kk / DB], acc[0][kk % DB]);
       __builtin_amdgcn_sched_barrier(0);
     });
-    wait_vmem();
+    wait_next(j + 2 < T);
   };
   auto sphase = [&](int j) {
-    if (j + 2 < T) issue_own(j + 2, (j + 2) % kPPStages);
+    if (j + 3 < T) issue_own(j + 3, (j + 3) % kPPStages);
     if (j + 1 < T) load_a(stage_of(j + 1));
     const int kt0 = j * kBQ;
     f32x16 p;
