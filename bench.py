@@ -34,10 +34,17 @@ REF_TFLOPS_N4096 = 34.36 / 0.8726   # reference db_full forward()+L, RTX 4060 Ti
 METRIC = "FA fwd TFLOP/s & % FP16 MFMA peak at B1 H8 N4096 D64; decode GB/s"
 
 
-def kernel_name(variant, D, causal=False, write_l=True, full=True):
-    """Template instance of the forward kernel behind a variant code."""
-    c, w, f = (str(x).lower() for x in (causal, write_l, full))
-    return f"fa_fwd_pp_kernel<{D},{c},{w},{f},{variant - 200}>"
+# Forward kernel variants: code -> (RING, TG) template arguments of
+# fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, RING, BF16, SPLITKV, TG>.
+VARIANT_ARGS = {204: (4, 2), 408: (8, 4)}
+
+
+def kernel_name(variant, D, causal=False, write_l=True, full=True, bf16=False):
+    """Template instance of the forward kernel behind a variant code, in the
+    form rocprofv3 prints (without the namespace and the spaces)."""
+    ring, tg = VARIANT_ARGS[variant]
+    c, w, f, b = (str(x).lower() for x in (causal, write_l, full, bf16))
+    return f"fa_fwd_pp_kernel<{D},{c},{w},{f},{ring},{b},false,{tg}>"
 
 
 def pmc_traffic(kernel):
@@ -324,20 +331,21 @@ def bench_sdpa(fa, torch, dev, reps=10):
 
 
 def bench_causal(fa, torch, dev, reps=7, iters=100):
-    """Causal D = 64 forward on one wave of workgroups: the default path
-    (row-block pairs, kernel variant 418) timed against the unpaired 64-row
-    kernel (variant 408, through the probe entry point) in alternating reps."""
+    """Causal D = 64 forward on one wave of 128-row workgroups: the default
+    path (the 64-row kernel, variant 408, on 256 CUs) timed against the
+    128-row kernel (variant 204, through the probe entry point) in
+    alternating reps."""
     res = {}
     for (B, H, N) in ((1, 8, 4096), (1, 16, 2048)):
         q, k, v = make_fwd(torch, dev, B, H, N, 64, seed=12)
         f = fwd_flops(B, H, N, 64, causal=True)
         d, u, delta = paired_delta(lambda: fa.forward(q, k, v, causal=True),
-                                   lambda: fa.probe.probe_fwd_variant(q, k, v, True, 408, True),
+                                   lambda: fa.probe.probe_fwd_variant(q, k, v, True, 204, True),
                                    reps, iters, torch)
         res[f"B{B}H{H}N{N}D64"] = {
             "ms": round(d, 5), "TFLOPs": round(f / d / 1e9, 1),
             "pct_peak": round(100 * f / d / 1e9 / PEAK_FP16_TFLOPS, 2),
-            "unpaired_408_ms": round(u, 5), "paired_median_delta_us": round(delta * 1000, 3)}
+            "kernel_204_ms": round(u, 5), "paired_median_delta_us": round(delta * 1000, 3)}
     return res
 
 

@@ -60,6 +60,8 @@ SIGNATURES = {
     "fa_probe_fwd_variant": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp]),
     "fa_probe_fwd_variants": (C.c_int, [_vp, C.c_int, _i64, C.c_int]),
     "fa_probe_default_variant": (C.c_int, [_i64]),
+    "fa_probe_choose_variant": (C.c_int, [_i64, C.c_int, _i64, _i64, C.c_int]),
+    "fa_probe_splitkv_plan_cus": (C.c_int, [_i64] * 4 + [C.c_int, C.c_int]),
     "fa_probe_read_bw": (C.c_int, [_vp, _i64, C.c_int, _vp, _vp]),
 }
 

@@ -42,13 +42,6 @@ namespace bwd {
 constexpr int kBQ = 64;     // rows of a streamed tile
 constexpr int kBlk = 128;   // rows owned by a workgroup (32 per wave)
 
-// Workgroup g of `total` runs logical block xcd-contiguously (see the forward).
-__device__ __forceinline__ int xcd_remap(int g, int total) {
-  const int q = total >> 3, r = total & 7;
-  const int xcd = g & 7, slot = g >> 3;
-  return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-}
-
 // Per-lane source offsets of 1 KiB block b of a 64-row tile, for the K-style
 // (row reads) and V-style (transposed reads) LDS swizzles.
 template <int D>
@@ -232,7 +225,7 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
   const int kw = wave & 3;
   const int grp = wave >> 2;
   const int hi = lane >> 5;
-  const int logical = xcd_remap(block, total);
+  const int logical = xcd_remap(block, total, geo.nxcd);
   const int bh = logical / num_kb;
   const int kb = logical - bh * num_kb;
   const int k0 = kb * kBlk;
@@ -411,7 +404,7 @@ __device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __
   const int qw = wave & 3;
   const int grp = wave >> 2;
   const int hi = lane >> 5;
-  const int logical = xcd_remap(block, total);
+  const int logical = xcd_remap(block, total, geo.nxcd);
   const int bh = logical / num_qb;
   int qb = logical - bh * num_qb;
   if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows first
@@ -588,7 +581,7 @@ __device__ __forceinline__ void dkdv_body_pp(const f16* __restrict__ Q, const f1
   const int grp = wave >> 2;                   // also this group's query half of a tile
   const int qb = grp;
   const int hi = lane >> 5;
-  const int logical = xcd_remap(block, total);
+  const int logical = xcd_remap(block, total, geo.nxcd);
   const int bh = logical / num_kb;
   const int kb = logical - bh * num_kb;
   const int k0 = kb * kBlk;
@@ -793,7 +786,7 @@ __device__ __forceinline__ void dq_body_pp(const f16* __restrict__ Q, const f16*
   const int grp = wave >> 2;                   // also this group's key half of a tile
   const int half = grp;
   const int hi = lane >> 5;
-  const int logical = xcd_remap(block, total);
+  const int logical = xcd_remap(block, total, geo.nxcd);
   const int bh = logical / num_qb;
   int qblk = logical - bh * num_qb;
   if (CAUSAL) qblk = num_qb - 1 - qblk;   // longest rows first
@@ -1022,9 +1015,9 @@ fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
   reinterpret_cast<f32x4*>(out)[i4] = acc;
 }
 
-// Units per half below which the D = 128 causal backward runs fused: two
-// per CU of MI355X's 256 (measured crossover, see launch_bwd).
-constexpr int kFuseUnitsD128 = 512;
+// Units per half, per CU, below which the D = 128 causal backward runs
+// fused: two (measured crossover on MI355X's 256 CUs, see launch_bwd).
+constexpr int kFuseUnitsPerCuD128 = 2;
 
 // Wave groups per workgroup: two (the second group takes the other half of
 // every tile, so the grid stays one workgroup per 128 rows and the SIMDs get
@@ -1046,7 +1039,7 @@ template <int D, bool CAUSAL, bool BF16>
 static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
                              float* ws, const Geom& geo, int64_t units, int64_t rows,
-                             int64_t out_heads, int64_t head_rows, hipStream_t s) {
+                             int64_t out_heads, int64_t head_rows, int cus, hipStream_t s) {
   const float scale = (float)(1.0 / sqrt((double)D));
   const float c = scale * kLog2e;
   const f16* Q = (const f16*)q;
@@ -1076,7 +1069,7 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   // the same length. (The fused D = 128 body also needs 4 VGPRs more than
   // the two budgets allow and spills them; the separate kernels do not.)
   if constexpr (GK == 2 && GQ == 2 && (D == 64 || CAUSAL)) {
-    if (D == 64 || total < kFuseUnitsD128) {
+    if (D == 64 || total < kFuseUnitsPerCuD128 * cus) {
       hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
                          s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
       launched = true;
@@ -1124,16 +1117,20 @@ namespace bwd {
 template <bool BF16>
 static int bwd_run(const void* q, const void* k, const void* v, const void* o, const void* dout,
                    const float* lse, float* dq, float* dk, float* dv, float* workspace,
-                   const Geom& geo, int64_t units, int64_t rows, int64_t out_heads,
+                   const Geom& geo_in, int64_t units, int64_t rows, int64_t out_heads,
                    int64_t head_rows, int64_t D, int causal, void* stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Topology topo = stream_topology(s);
+  Geom geo = geo_in;
+  geo.nxcd = topo.xcds;
+  const int cus = topo.cus;
   hipError_t e;
   if (D == 64) {
-    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s)
-               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s);
+    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s)
+               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s);
   } else {
-    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s)
-               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s);
+    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s)
+               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s);
   }
   return e == hipSuccess ? FA_OK : -(int)e;
 }

@@ -9,10 +9,9 @@
 //
 // Work decomposition (CDNA4):
 //   * a workgroup owns 128 query rows of one (b, h), 8 waves (64 rows with
-//     four key-tile groups where 128-row blocks leave CUs idle, and causal
-//     row blocks i and num_qb - 1 - i together on a single wave of
-//     workgroups); a 1-D grid with an XCD-aware remap keeps the query blocks
-//     of a head on one XCD so its K/V stay in that XCD's L2;
+//     four key-tile groups where 128-row blocks leave CUs idle); a 1-D grid
+//     with an XCD-aware remap keeps the query blocks of a head on one XCD so
+//     its K/V stay in that XCD's L2;
 //   * K/V advance in 64-key tiles, copied global -> LDS by buffer_load ... lds
 //     into rings of LDS slots while earlier tiles are consumed; every LDS
 //     operand read has a constant offset from a per-lane base;
@@ -27,7 +26,7 @@
 // so each SIMD runs one wave's MFMAs while the other wave's VALU work issues.
 // Template flags: D in {64,128}, CAUSAL, WRITE_L (O-only when false), FULL
 // (N a multiple of the variant's full-tile unit: no bounds predicates), BF16,
-// SPLITKV, TG (key-tile groups), PAIR (causal row-block pairs).
+// SPLITKV, TG (key-tile groups).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -45,14 +44,6 @@ constexpr int kBC = 64;    // keys per tile
 // A lane's tile sum of P above this triggers a rescale; it bounds every P,
 // so P stays far inside the fp16 range (65504).
 constexpr float kSumLimit = 32768.0f;
-
-// Workgroup g of `total` lands on XCD g % 8. Map it to a logical tile index
-// so that each XCD gets one contiguous range of logical tiles.
-__device__ __forceinline__ int xcd_remap(int g, int total) {
-  const int q = total >> 3, r = total & 7;
-  const int xcd = g & 7, slot = g >> 3;
-  return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-}
 
 // State and tile operations of one wave: 32 query rows, one lane pair per row
 // (lanes l and l^32 hold the two halves of every 32-key block).
@@ -353,49 +344,8 @@ struct RowBlock {
       Lh[qrow] = (m_run + log2_hw(l_tot)) * kLn2;
   }
 
-  // Combine the two half-rows, normalise and store O (and L), staged through
-  // this wave's `stage` LDS area (at least 32 rows of STAGE_STRIDE bytes,
-  // written and read only by this wave):
-  // each lane writes its 16-byte chunks, then 8 lanes store one 128-byte
-  // (D = 64) or two (D = 128) rows, so a store instruction covers whole rows
-  // instead of 32-byte pieces of 32 rows.
-  static constexpr int STAGE_STRIDE = 2 * D + 16;   // padded: spreads the LDS banks
-  template <bool WRITE_L>
-  __device__ __forceinline__ void finish_staged(f16* Oh, float* Lh, char* stage) const {
-    const float l_tot = sum_xor32(l_run);
-    const float inv = 1.f / l_tot;
-    constexpr int CPR = D / 8;                       // 16-byte chunks per row
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int gp = 0; gp < 2; ++gp) {
-        uint32_t w[2][2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int g = 2 * gp + j;
-          const f16x2 a = cvt2x<BF16>(o[db][4 * g + 0] * inv, o[db][4 * g + 1] * inv);
-          const f16x2 b = cvt2x<BF16>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-          w[j][0] = __builtin_bit_cast(uint32_t, a);
-          w[j][1] = __builtin_bit_cast(uint32_t, b);
-        }
-        const auto r0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
-        const auto r1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
-        const int chunk = 4 * db + 2 * gp + hi;      // 16-byte chunk of the row
-        *reinterpret_cast<uint4*>(stage + (lane & 31) * STAGE_STRIDE + chunk * 16) =
-            uint4{r0[0], r1[0], r0[1], r1[1]};
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS writes landed
-#pragma unroll
-    for (int k = 0; k < 32 * CPR / 64; ++k) {
-      const int idx = 64 * k + lane;
-      const int r = idx / CPR, ch = idx % CPR;
-      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * STAGE_STRIDE + ch * 16);
-      if (FULL || row_w + r < N)
-        *reinterpret_cast<uint4*>(Oh + (size_t)(row_w + r) * D + ch * 8) = v;
-    }
-    if (WRITE_L && hi == 0 && (FULL || qrow < N)) Lh[qrow] = (m_run + log2_hw(l_tot)) * kLn2;
-  }
+  // Rows of the O staging tile are padded by 16 bytes: spreads the LDS banks.
+  static constexpr int STAGE_STRIDE = 2 * D + 16;
 
   // Split-KV epilogue: this row's fp32 O normalised over the keys of one
   // split and the natural-log LSE of those keys, at partial index `at` of a
@@ -508,19 +458,9 @@ __device__ __forceinline__ void dma_block_or_zero(const char* head, int head_byt
 // SPLITKV: the grid covers (row block, key range) units; each writes fp32
 // partials normalised over its range and the range's LSE, merged by the LSE
 // combine afterwards.
-//
-// PAIR (causal, four tile groups): workgroup i of a head owns row blocks
-// A = num_qb - 1 - i and B = i, whose triangles add up to num_qb + 1 tiles,
-// so every workgroup of the grid has the same work. One pipeline runs over
-// A's tiles (rounded up to whole steps, the extra ones past A's diagonal
-// and masked) and then B's: step jb's matrix phase does A's last PV and B's
-// first QK, and each wave then keeps A's state aside until the merge, where
-// tile group 0 finishes A and tile group 1 finishes B. No second prologue,
-// pipeline fill and drain, or workgroup launch per row block; one loop body
-// serves both blocks (a second copy of the loop ran cold and slower).
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, bool WRITE_L, bool FULL, int RING, bool BF16 = false,
-          bool SPLITKV = false, int TG = 2, bool PAIR = false>
+          bool SPLITKV = false, int TG = 2>
 __global__ void __launch_bounds__(512)
 fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, f16* __restrict__ O,
@@ -535,7 +475,6 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int LOADS = BLOCKS / NRG;          // blocks per M-phase wave per tile
   static_assert(TG == 2 || TG == 4, "two or four tile groups");
   static_assert(!SPLITKV || TG == 2, "split-KV runs with two tile groups");
-  static_assert(!PAIR || (CAUSAL && TG == 4 && !SPLITKV), "row-block pairs: causal, four tile groups");
   // Two steps of slots: a copy lands one step ahead of its read, and the
   // prologue's waits below are counted for this ring.
   static_assert(RING == 2 * TG, "a ring of two steps");
@@ -559,16 +498,13 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // This wave's tile in step j.
   auto tile_of = [&](int j) { return TG * j + tg; };
 
-  const int logical = xcd_remap(blockIdx.x, total);
+  const int logical = xcd_remap(blockIdx.x, total, geo.nxcd);
   // Split-KV: the splits of one q-block are adjacent (same XCD, same K/V).
   const int split = SPLITKV ? logical % nsplit : 0;
   const int unit = SPLITKV ? logical / nsplit : logical;
-  const int per_head = PAIR ? (num_qb + 1) >> 1 : num_qb;   // workgroups per head
-  const int bh = unit / per_head;
-  int qb = unit - bh * per_head;
-  const int qb_b = qb;                // PAIR: row block B
-  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first (PAIR: A)
-  const bool has_b = PAIR && qb_b < qb;   // an odd num_qb leaves one block unpaired
+  const int bh = unit / num_qb;
+  int qb = unit - bh * num_qb;
+  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows dispatch first
 
   const HeadView hv = head_view<D>(geo, bh);
   const int N = hv.n;
@@ -579,21 +515,9 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 
   RB rb;
   rb.init(Q + head, head_bytes, lane, q0 + 32 * rg, N, c);
-  // PAIR: B's Q fragments and rows (rb takes them over at the switch), and
-  // A's rows, whose O, m and l move here at the switch.
-  RB rbb, ra;
-  if constexpr (PAIR) {
-    rbb.init(Q + head, head_bytes, lane, qb_b * ROWS + 32 * rg, N, c);
-    ra = rb;
-  }
 
   const int kv_end = CAUSAL ? min(N, q0 + ROWS) : N;
   int n_tiles = (kv_end + kBC - 1) / kBC;
-  // PAIR: A's tiles fill steps [0, jb) (tiles n_tiles .. 4 jb - 1 lie past
-  // A's diagonal); B's key tile k is pipeline tile 4 jb + k.
-  const int jb = (n_tiles + TG - 1) / TG;
-  const int n_b = has_b ? qb_b + 1 : 0;
-  const int b0 = TG * jb;
   // Split-KV: this workgroup's tiles are tb .. tb + n_tiles - 1 of the row
   // block's; K/V pointers and bounds start at tile tb, masking uses absolute
   // key positions.
@@ -611,10 +535,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   const char* Kh = reinterpret_cast<const char*>(K + hv.kv) + (size_t)tb * TILE;
   const char* Vh = reinterpret_cast<const char*>(V + hv.kv) + (size_t)tb * TILE;
   // Tiles per tile group.
-  const int n_steps = PAIR ? jb + (n_b + TG - 1) / TG : (n_tiles + TG - 1) / TG;
-  // Key tile of pipeline tile u, and whether it holds keys of its row block.
-  auto key_tile = [&](int u) { return (PAIR && u >= b0) ? u - b0 : u; };
-  auto tile_live = [&](int u) { return (PAIR && u >= b0) ? u - b0 < n_b : u < n_tiles; };
+  const int n_steps = (n_tiles + TG - 1) / TG;
 
   const uint32_t lds0 = lds_addr(smem);
   // This wave's share of a tile copy in its M phase: blocks rg*LOADS .. +LOADS.
@@ -623,7 +544,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   for (int i = 0; i < LOADS; ++i) dma_offsets<D>(rg * LOADS + i, lane, koff[i], voff[i]);
   // 1 KiB block b of tile t, bounded by the range (zeros past the end).
   auto dma_tile_block = [&](bool is_v, int t, uint32_t dst, uint32_t off) {
-    dma_block_or_zero<D, FULL>(is_v ? Vh : Kh, kv_bytes, key_tile(t), tile_live(t), dst, off);
+    dma_block_or_zero<D, FULL>(is_v ? Vh : Kh, kv_bytes, t, t < n_tiles, dst, off);
   };
   auto copy_block = [&](bool is_v, int t, int i) {
     const uint32_t at = lds0 + ((is_v ? RING : 0) + t % RING) * TILE + (rg * LOADS + i) * 1024;
@@ -725,7 +646,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       wait_vmcnt<((RING - TG) / TG - 1) * 2 * LOADS>();
       return;
     }
-    rb.template mask<2>(tb + key_tile(t), 0, s);
+    rb.template mask<2>(tb + t, 0, s);
     const float m_cur = rb.m_run;
     constexpr int PAIRS = 8 * NB;
     float ex[PAIRS][2];
@@ -776,26 +697,6 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   auto mstep = [&](auto with_pv, int tq, int tv) {
     mphase(with_pv, tq, tv, tq + RING - TG, tv + RING - TG);
   };
-  // PAIR: the matrix phase that crosses from A to B (A's last PV, B's first
-  // QK) takes B's Q fragments before it; after it A's O, m and l move aside
-  // and B's rows start empty. One loop body serves both row blocks.
-  auto take_q_b = [&] {
-#pragma unroll
-    for (int k = 0; k < KSTEPS; ++k) rb.qf[k] = rbb.qf[k];
-  };
-  auto switch_rows = [&] {
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      ra.o[db] = rb.o[db];
-      rb.o[db] = f32x16{};
-    }
-    ra.m_run = rb.m_run;
-    ra.l_run = rb.l_run;
-    rb.m_run = -INFINITY;
-    rb.l_run = 0.f;
-    rb.row_w = rbb.row_w;
-    rb.qrow = rbb.qrow;
-  };
   if (grp == 0) {
     rb.template qk<NB>(smem + (tile_of(0) % RING) * TILE, 0, s);
     __syncthreads();                 // its slot is refilled in phase 1
@@ -804,12 +705,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       sphase(tile_of(j));
       pin_p();
       __syncthreads();
-      // PAIR: step jb - 1 crosses (for an unpaired block its QK reads a tile
-      // past the end, as a last step does).
-      const bool cross = PAIR && j == jb - 1;
-      if (cross) take_q_b();
       mstep(BT{}, tile_of(j + 1), tile_of(j));
-      if (cross) switch_rows();
       __syncthreads();
     }
     __syncthreads();   // group 1's last PV
@@ -824,11 +720,7 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
     pin_p();
     __syncthreads();
     for (int j = 1; j < n_steps; ++j) {
-      // PAIR: step jb crosses (if B has tiles).
-      const bool cross = PAIR && j == jb;
-      if (cross) take_q_b();
       mstep(BT{}, tile_of(j), tile_of(j - 1));
-      if (cross) switch_rows();
       __syncthreads();
       pin_s();
       sphase(tile_of(j));
@@ -842,9 +734,6 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
       for (int i = 0; i < NMM; ++i) rb.o[i % DB] = mma32<BF16>(vblk_frag(vl + i * 1024), p[i / DB], rb.o[i % DB]);
     }
     __syncthreads();
-    if constexpr (PAIR) {
-      if (jb == n_steps) switch_rows();   // unpaired block: A's state in place
-    }
   }
   wait_vmem();   // copies of the last M phases
 
@@ -858,37 +747,6 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   constexpr int PREC = RB::template part_rec_floats<TG>();
   constexpr int RECS = TG * NRG * PREC;                 // floats of one row block's records
   constexpr int STAGE_BYTES = NRG * 32 * RB::STAGE_STRIDE;
-  if constexpr (PAIR) {
-    // Tile group 0 merges A's rows from the records of groups 1 .. 3 and
-    // tile group 1 B's from groups 0, 2, 3, in parallel, with full records
-    // (the part merge above measured slower here: four waves in two passes,
-    // or 236 VGPRs with one merge instance per row block); each finishing
-    // wave stages its O tile in its first record, once read.
-    constexpr int NREC = (TG - 1) * NRG;
-    static_assert(2 * NREC * REC * 4 <= 2 * RING * TILE, "merge area too small");
-    auto rec_a = [&](int g) { return area + ((g - 1) * NRG + rg) * REC; };
-    auto rec_b = [&](int g) { return area + (NREC + (g == 0 ? 0 : g - 1) * NRG + rg) * REC; };
-    if (tg != 0) ra.save_to(rec_a(tg));
-    if (has_b && tg != 1) rb.save_to(rec_b(tg));
-    __syncthreads();
-    if (tg >= 2 || (tg == 1 && !has_b)) return;
-    // One merge and store path: tile group 0 brings A's state into rb.
-    if (tg == 0) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) rb.o[db] = ra.o[db];
-      rb.m_run = ra.m_run;
-      rb.l_run = ra.l_run;
-      rb.row_w = ra.row_w;
-      rb.qrow = ra.qrow;
-    }
-    float* r0 = tg == 0 ? rec_a(1) : rec_b(0);
-    rb.merge_from(r0);
-    rb.merge_from(tg == 0 ? rec_a(2) : rec_b(2));
-    rb.merge_from(tg == 0 ? rec_a(3) : rec_b(3));
-    static_assert(32 * RB::STAGE_STRIDE <= REC * 4, "O staging exceeds the merge record");
-    rb.template finish_staged<WRITE_L>(O + head, L + hv.l, reinterpret_cast<char*>(r0));
-    return;
-  }
   if constexpr (!SPLITKV) {
     static_assert(RECS * 4 + STAGE_BYTES <= 2 * RING * TILE, "merge area too small");
     auto rec = [&](int i) { return area + (i * NRG + rg) * PREC; };
@@ -916,26 +774,21 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 // Kernel variants (for fa_probe_fwd_variant; the default path picks one per
 // problem shape): the ping-pong kernel with two tile groups over 128 rows and
 // a ring of 4 tiles (204), or with four tile groups over 64 rows and a ring
-// of 8 tiles (408, D = 64: twice the workgroups for the same rows), or the
-// 408 kernel over pairs of causal row blocks i and num_qb - 1 - i (418).
+// of 8 tiles (408, D = 64: twice the workgroups for the same rows).
 constexpr int kPingPong = 204;
 constexpr int kPingPong4 = 408;
-constexpr int kPairs4 = 418;
 constexpr int kGuarded = 1000;   // probe flag: force the guarded (not full-tile) instance
 
 // Query rows per row block, and the multiple of N that lets every tile group
-// run the same number of whole tiles (the full-tile instance; causal pairs
-// mask the tiles past each diagonal anyway, so whole tiles suffice).
-static int variant_rows(int variant) { return variant == kPingPong4 || variant == kPairs4 ? 64 : kBR; }
-static int variant_full_n(int variant) {
-  return variant == kPingPong4 ? 256 : variant == kPairs4 ? kBC : kBR;
-}
+// run the same number of whole tiles (the full-tile instance).
+static int variant_rows(int variant) { return variant == kPingPong4 ? 64 : kBR; }
+static int variant_full_n(int variant) { return variant == kPingPong4 ? 256 : kBR; }
 
 // Variants that exist for head dimension D and the causal flag.
 static bool variant_fits(int D, int variant, int causal) {
   if (variant == kPingPong) return true;
   if (variant == kPingPong4) return D == 64;
-  if (variant == kPairs4) return D == 64 && causal;
+  (void)causal;
   return false;
 }
 
@@ -962,13 +815,6 @@ static hipError_t launch_fwd(const void* q, const void* k, const void* v, void* 
         break;
       }
       return hipErrorInvalidValue;
-    case kPairs4:
-      if constexpr (D == 64 && CAUSAL) {
-        hipLaunchKernelGGL((fa_fwd_pp_kernel<D, CAUSAL, WRITE_L, FULL, 8, BF16, false, 4, true>),
-                           dim3(total), dim3(512), 0, stream, Q, K, V, Op, lse, geo, num_qb, total, c);
-        break;
-      }
-      return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
   }
@@ -991,26 +837,21 @@ static hipError_t dispatch_wl(const void* q, const void* k, const void* v, void*
                                                           variant, s);
 }
 
-constexpr int kNumCUs = 256;   // MI355X
-
 // The kernel the forward runs for a problem shape (bh = B * H heads of N
-// rows), fixed per build: nothing in the environment changes it. Measured on
-// MI355X (D = 64, us, 128-row vs 64-row workgroups): where the 128-row grid
-// leaves CUs idle the 64-row kernel wins (B1 H8 N2048 17.3 -> 13.8, B1 H4
-// N4096 29.7 -> 22.9, B1 H16 N1024 11.3 -> 9.6), and so it does for causal
-// long rows on a single wave of workgroups (B1 H8 N4096 33.6 -> 29.0, the
-// short row blocks finish early and free their CUs); from 256 row blocks
-// of 128 on (non-causal) or 512 (causal) it loses (B1 H16 N2048 21.1 vs 26.5,
-// B2 H8 N4096 causal 45.1 vs 55.5), as it does for causal N = 1024 (B4 H8
-// 12.8 vs 17.6). On that single causal wave, pairs of row blocks (418, dense
-// batches only) beat separate 64-row workgroups: B1 H8 N4096 30.3 -> 28.1,
-// B1 H16 N2048 21.1 -> 19.7 (same-process A/B); on two or more waves the
-// 128-row kernel still wins (B2 H8 N4096 47.6 vs 56.1).
-static int choose_variant(int64_t D, int causal, int64_t bh, int64_t N, bool dense) {
+// rows) on a device of `cus` compute units; nothing in the environment
+// changes it. Measured on MI355X (256 CUs; D = 64, us, 128-row vs 64-row
+// workgroups): where the 128-row grid leaves CUs idle the 64-row kernel wins
+// (B1 H8 N2048 17.3 -> 13.8, B1 H4 N4096 29.7 -> 22.9, B1 H16 N1024 11.3 ->
+// 9.6), and so it does for causal long rows on a single wave of workgroups
+// (B1 H8 N4096 33.6 -> 29.0: the short row blocks finish early and free their
+// CUs); from one 128-row block per CU on (non-causal) or two (causal) it
+// loses (B1 H16 N2048 21.1 vs 26.5, B2 H8 N4096 causal 45.1 vs 55.5), as it
+// does for causal N = 1024 (B4 H8 12.8 vs 17.6).
+static int choose_variant(int64_t D, int causal, int64_t bh, int64_t N, int cus) {
   if (D != 64) return kPingPong;
   const int64_t grid = bh * ((N + kBR - 1) / kBR);
-  if (grid < kNumCUs) return kPingPong4;
-  if (causal && grid == kNumCUs && N >= 2048) return dense ? kPairs4 : kPingPong4;
+  if (grid < cus) return kPingPong4;
+  if (causal && grid == cus && N >= 2048) return kPingPong4;
   return kPingPong;
 }
 
@@ -1020,25 +861,25 @@ namespace fa {
 // The forward over a head geometry with an explicit kernel variant (0: the
 // default choice). Arguments are already validated.
 static int fwd_run(const void* q, const void* k, const void* v, void* o, float* lse,
-                   const Geom& geo, int64_t B, int64_t D, int causal, int variant, void* stream,
+                   const Geom& geo_in, int64_t B, int64_t D, int causal, int variant, void* stream,
                    bool bf16 = false) {
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Topology topo = stream_topology(s);
+  Geom geo = geo_in;
+  geo.nxcd = topo.xcds;
   // kGuarded + v: variant v through its guarded instance even where N is a
   // multiple of the row block (tests compare it bitwise with the full-tile one).
   const bool guarded = variant >= kGuarded;
   if (guarded) variant -= kGuarded;
-  if (variant == 0) variant = choose_variant(D, causal, B * geo.H, geo.N, geo.cu == nullptr);
+  if (variant == 0) variant = choose_variant(D, causal, B * geo.H, geo.N, topo.cus);
   if (!variant_fits((int)D, variant, causal)) return FA_ERR_HEAD_DIM;
-  // Pairs need every row block of a head present (a dense batch).
-  if (variant == kPairs4 && geo.cu != nullptr) return FA_ERR_HEAD_DIM;
   const int rows = variant_rows(variant);
   const int num_qb = (geo.N + rows - 1) / rows;
   // The validation bounds the grid of 128-row blocks; 64-row blocks double it.
   if (B * geo.H * (int64_t)num_qb > (int64_t(1) << 31) - 1) return FA_ERR_TOO_LARGE;
-  const int per_head = variant == kPairs4 ? (num_qb + 1) / 2 : num_qb;   // workgroups
-  const int total = (int)(B * geo.H * per_head);
+  const int total = (int)(B * geo.H * num_qb);   // workgroups
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   const bool full = !guarded && geo.cu == nullptr && (geo.N % variant_full_n(variant)) == 0;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
 #define FA_FWD_DISPATCH(DD, CC, BB) \
   dispatch_wl<DD, CC, BB>(q, k, v, o, lse, geo, num_qb, total, c, full, variant, s)
@@ -1084,8 +925,10 @@ static hipError_t launch_splitkv(const f16* Q, const f16* K, const f16* V, f16* 
 }
 }  // namespace fa
 
-extern "C" int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal) {
-  if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128)) return 1;
+namespace fa {
+// Key splits for the torch forward on a device of `cus` compute units.
+static int splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int cus) {
+  if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128) || cus <= 0) return 1;
   // Measured: a split pays where the row blocks leave CUs idle and each split
   // still has >= 32 key tiles (B1 H1 N16384: 122 -> 88 us with 2 splits);
   // with fewer tiles per workgroup its fixed costs and the combine pass
@@ -1097,13 +940,30 @@ extern "C" int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, i
   // N8192 42.0 vs 49.5, B1 H1 N8192 31.6 vs 32.0 with 4, B1 H2 N4096 18.8 vs
   // 23.1 with 4).
   if (D == 64) return 1;
-  const int64_t units = B * H * ((N + fa::kBR - 1) / fa::kBR);
-  const int64_t tiles = (N + fa::kBC - 1) / fa::kBC;   // key tiles of a row block
-  if (units >= fa::kNumCUs) return 1;
-  int64_t sp = (fa::kNumCUs + units - 1) / units;
+  const int64_t units = B * H * ((N + kBR - 1) / kBR);
+  const int64_t tiles = (N + kBC - 1) / kBC;   // key tiles of a row block
+  if (units >= cus) return 1;
+  int64_t sp = (cus + units - 1) / units;
   sp = sp < tiles / 32 ? sp : tiles / 32;
   sp = sp < 8 ? sp : 8;
   return sp < 2 ? 1 : (int)sp;
+}
+}  // namespace fa
+
+extern "C" int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  return fa::splitkv_plan(B, H, N, D, causal, fa::device_topology(dev).cus);
+}
+
+extern "C" int fa_probe_splitkv_plan_cus(int64_t B, int64_t H, int64_t N, int64_t D, int causal,
+                                         int cus) {
+  return fa::splitkv_plan(B, H, N, D, causal, cus);
+}
+
+extern "C" int fa_probe_choose_variant(int64_t D, int causal, int64_t bh, int64_t N, int cus) {
+  if ((D != 64 && D != 128) || bh <= 0 || N <= 0 || cus <= 0) return 0;
+  return fa::choose_variant(D, causal, bh, N, cus);
 }
 
 extern "C" int64_t fa_fwd_splitkv_workspace_floats(int64_t B, int64_t H, int64_t N, int64_t D,
@@ -1125,7 +985,7 @@ extern "C" int fa_fwd_splitkv_f16(const void* q, const void* k, const void* v, v
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
   const int64_t num_qb = (N + kBR - 1) / kBR;
   if (B * H * num_qb > (int64_t(1) << 31) / num_splits) return FA_ERR_TOO_LARGE;
-  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0, 0, 1};
   const int units = (int)(B * H * num_qb);
   const float c = (float)(1.0 / sqrt((double)D)) * kLog2e;
   const bool full = (N % kBR) == 0;
@@ -1137,6 +997,7 @@ extern "C" int fa_fwd_splitkv_f16(const void* q, const void* k, const void* v, v
   const f16* V = (const f16*)v;
   f16* Op = (f16*)o;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  geo.nxcd = stream_topology(s).xcds;
   const int ns = (int)num_splits;
   const int nq = (int)num_qb;
   hipError_t e;
@@ -1197,11 +1058,13 @@ extern "C" int fa_probe_fwd_variant(const void* q, const void* k, const void* v,
 
 extern "C" int fa_probe_default_variant(int64_t D) {
   if (D != 64 && D != 128) return 0;
-  return fa::choose_variant(D, 0, 8, 4096, true);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  return fa::choose_variant(D, 0, 8, 4096, fa::device_topology(dev).cus);
 }
 
 extern "C" int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal) {
-  static const int all[] = {204, 408, 418};
+  static const int all[] = {204, 408};
   int n = 0;
   for (int v : all) {
     if (fa::variant_fits((int)D, v, causal)) {

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 namespace fa {
@@ -321,7 +322,55 @@ struct Geom {
   int group;
   int total;
   int B;       // varlen: number of sequences
+  int nxcd;    // XCDs of the device the launch runs on (set by the launcher)
 };
+
+// Workgroup g of a 1-D grid of `total` lands on XCD g % nxcd (the dispatcher
+// deals consecutive workgroups to the XCDs in turn). Map it to a logical index
+// so that each XCD gets one contiguous range of logical indices: the row
+// blocks of a head then share one XCD's L2, which serves their K/V after the
+// first fetch. nxcd <= 1 (one XCD, or a partition of one) is the identity.
+__device__ __forceinline__ int xcd_remap(int g, int total, int nxcd) {
+  if (nxcd <= 1) return g;
+  const int q = total / nxcd, r = total % nxcd;
+  const int xcd = g % nxcd, slot = g / nxcd;
+  return (xcd < r) ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
+// Compute units and XCDs of a device: read once per device from the runtime
+// (hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeNumberOfXccs) and
+// kept for later calls. A partitioned MI355X reports its own share (e.g. 32
+// CUs on one XCD per partition), so the kernel choices and the XCD remap
+// follow the device the launch actually runs on.
+struct Topology {
+  int cus;
+  int xcds;
+};
+
+inline Topology device_topology(int dev) {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];   // cus << 8 | xcds, 0 = not read yet
+  const bool cacheable = dev >= 0 && dev < kMaxDev;
+  if (cacheable) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v != 0) return Topology{v >> 8, v & 0xff};
+  }
+  int cus = 0, xcds = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;   // MI355X, if the runtime cannot say
+  if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || xcds <= 0)
+    xcds = 1;
+  if (xcds > 255) xcds = 255;
+  if (cacheable) cache[dev].store(cus << 8 | xcds, std::memory_order_relaxed);
+  return Topology{cus, xcds};
+}
+
+// Topology of the device that runs work queued on `stream`.
+inline Topology stream_topology(hipStream_t stream) {
+  int dev = 0;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess && hipGetDevice(&dev) != hipSuccess) dev = 0;
+  return device_topology(dev);
+}
 
 // One (b, h): element offsets of its Q/O and K/V rows, of its L row, and its
 // length. Varlen bounds are clamped into [0, total] and to N, so a malformed

@@ -125,7 +125,10 @@ int fa_validate_fwd_varlen(const void* q, const void* k, const void* v, const vo
  * max_seqlen sizes the grid and must be >= every sequence length: rows past
  * it are not computed. Bounds read from cu_seqlens are clamped into
  * [0, total], so a malformed table cannot move any access outside the
- * buffers. No reference counterpart (README.md:326 lists varlen as not
+ * buffers. Rows of o and lse that belong to no sequence (rows before
+ * cu_seqlens[0] or from cu_seqlens[B] on) are never written: a caller that
+ * needs them defined sets O = 0 and L = -inf there itself (the torch binding
+ * does). No reference counterpart (README.md:326 lists varlen as not
  * covered).
  */
 int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -220,7 +223,8 @@ int fa_validate_bwd_varlen(const void* q, const void* k, const void* v, const vo
  * forward's tolerance of the unsplit kernel; lse nullable (O only). The
  * workspace (fa_fwd_splitkv_workspace_floats floats, 16-byte aligned) holds
  * the fp32 partials. fa_fwd_splitkv_plan returns the split count the torch
- * binding uses (1: no split) for a shape.
+ * binding uses (1: no split) for a shape on the current device (it depends on
+ * the device's compute-unit count).
  */
 int fa_fwd_splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal);
 int64_t fa_fwd_splitkv_workspace_floats(int64_t B, int64_t H, int64_t N, int64_t D,

@@ -7,11 +7,19 @@
  *
  * All buffers are device pointers; every probe runs one wave on `stream`.
  * Return: 0 ok, > 0 bad argument, < 0 negated hipError_t.
+ *
+ * Probe interface version FA_PROBE_VERSION (separate from the product ABI's
+ * fa_abi_version): 2 added the causal argument of fa_probe_fwd_variants;
+ * 3 removed variant 418 and added fa_probe_choose_variant and
+ * fa_probe_splitkv_plan_cus (the kernel and split choices for a given
+ * compute-unit count, without a device).
  */
 #ifndef FA_PROBE_H
 #define FA_PROBE_H
 
 #include <stdint.h>
+
+#define FA_PROBE_VERSION 3
 
 #ifdef __cplusplus
 extern "C" {
@@ -54,13 +62,21 @@ int fa_probe_fwd_variant(const void* q, const void* k, const void* v, void* o, f
                          void* stream);
 
 /* The variant fa_fwd_f16 runs for head dimension D at the headline shape
- * (B = 1, H = 8, N = 4096, non-causal; 0 for another D). 204 = ping-pong
- * kernel with two tile groups over 128 rows (ring of 4 tiles), 408 = with
- * four tile groups over 64 rows (ring of 8 tiles, D = 64); the forward picks
- * 408 for D = 64 where 128-row workgroups leave CUs idle. 418 (causal, D = 64,
- * dense batches only) = the 408 kernel over pairs of causal row blocks i and
- * ceil(N/64) - 1 - i, one workgroup per pair. */
+ * (B = 1, H = 8, N = 4096, non-causal) on the current device (0 for another
+ * D). 204 = ping-pong kernel with two tile groups over 128 rows (ring of 4
+ * tiles), 408 = with four tile groups over 64 rows (ring of 8 tiles,
+ * D = 64); the forward picks 408 for D = 64 where 128-row workgroups leave
+ * CUs idle. */
 int fa_probe_default_variant(int64_t D);
+
+/* The variant the forward picks for bh = B*H heads of N rows on a device of
+ * `cus` compute units (the device's own count is read at launch time).
+ * 0 for a bad argument. No device needed. */
+int fa_probe_choose_variant(int64_t D, int causal, int64_t bh, int64_t N, int cus);
+
+/* fa_fwd_splitkv_plan for a device of `cus` compute units instead of the
+ * current device's. No device needed. */
+int fa_probe_splitkv_plan_cus(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int cus);
 
 /* Writes up to max_out variant codes that exist for head dimension D and the
  * causal flag into out (may be NULL) and returns how many there are. */

@@ -1,7 +1,7 @@
 """GPU tier: the bfloat16 paths against the CPU oracle: forward (forward_bf16,
 which picks its kernel from the shape as the fp16 forward does: the D = 64
-cases run the 64-row kernel, the 128-row one at N = 4096 and, causal there,
-the row-block pairs),
+cases run the 64-row kernel, the 128-row one at N = 4096 (and the 64-row one
+again, causal there)),
 backward (backward_bf16), paged decode and page writer (decode_paged and
 kv_append with bf16 tensors).
 

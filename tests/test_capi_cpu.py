@@ -318,3 +318,38 @@ def test_read_probe_rejects_before_touching_the_device(capi):
     assert lib.fa_probe_read_bw(A, 0, 8, A, None) == 2
     assert lib.fa_probe_read_bw(A, 1024, 0, A, None) == 2     # no workgroups
     assert lib.fa_probe_read_bw(A + 8, 1024, 8, A, None) == 2  # 8-byte aligned only
+
+
+def test_kernel_and_split_choice_follow_the_cu_count(capi):
+    """The forward's kernel variant and key-split count come from the device's
+    compute-unit count (read at launch), not from a built-in 256: the same
+    shape on a 256-CU MI355X and on a 32-CU partition (one XCD) chooses
+    differently, and both choices follow the measured crossovers."""
+    lib = capi.load()
+    choose, plan = lib.fa_probe_choose_variant, lib.fa_probe_splitkv_plan_cus
+    # D = 128 always runs the 128-row kernel
+    assert choose(128, 0, 8, 4096, 256) == 204 and choose(128, 1, 1, 64, 32) == 204
+    # D = 64 at 256 CUs: fewer 128-row blocks than CUs -> the 64-row kernel
+    assert choose(64, 0, 8, 2048, 256) == 408      # 128 blocks < 256
+    assert choose(64, 0, 8, 4096, 256) == 204      # 256 blocks = one per CU
+    assert choose(64, 1, 8, 4096, 256) == 408      # causal, exactly one wave, N >= 2048
+    assert choose(64, 1, 16, 4096, 256) == 204     # causal, two waves
+    assert choose(64, 1, 32, 1024, 256) == 204     # causal, one wave but N < 2048
+    # the same shapes on a 32-CU device: 128 and 256 blocks fill it several times
+    assert choose(64, 0, 8, 2048, 32) == 204
+    assert choose(64, 1, 8, 4096, 32) == 204
+    assert choose(64, 0, 1, 2048, 32) == 408       # 16 blocks < 32
+    assert choose(64, 0, 1, 4096, 32) == 204       # exactly 32 blocks
+    assert choose(64, 1, 1, 4096, 32) == 408       # causal, one wave of 32
+    # bad arguments
+    assert choose(96, 0, 8, 4096, 256) == 0 and choose(64, 0, 8, 4096, 0) == 0
+    # split-KV plan: D = 128 long sequences over few heads split to fill the CUs
+    assert plan(1, 1, 16384, 128, 0, 256) == 2     # 128 blocks, 256 tiles / 32 = 8 -> ceil(256/128)
+    assert plan(1, 1, 16384, 128, 0, 32) == 1      # 128 blocks >= 32 CUs
+    assert plan(1, 1, 4096, 128, 0, 256) == 2      # 32 blocks: 8 by CUs, 64 tiles / 32 = 2
+    assert plan(1, 1, 4096, 128, 0, 64) == 2
+    assert plan(1, 1, 2048, 128, 0, 256) == 1      # 32 tiles: too few per split
+    assert plan(1, 8, 4096, 128, 0, 256) == 1      # 256 blocks fill 256 CUs
+    assert plan(1, 8, 4096, 128, 0, 512) == 2      # but not a 512-CU device
+    assert plan(1, 1, 16384, 64, 0, 256) == 1      # D = 64 never splits
+    assert plan(1, 1, 16384, 128, 1, 256) == 1     # causal never splits

@@ -42,10 +42,10 @@ def test_gqa_forward(fa, dev, D, Hkv, N, causal):
 
 
 @pytest.mark.parametrize("Hkv", [4, 1])
-def test_gqa_causal_row_block_pairs(fa, dev, Hkv):
-    """B1 H16 N2048 D64 causal: the default path runs the row-block pairs
-    (one workgroup per pair of 64-row blocks i and 31 - i), here with K/V
-    heads shared by groups of query heads."""
+def test_gqa_causal_single_wave(fa, dev, Hkv):
+    """B1 H16 N2048 D64 causal (one wave of 128-row blocks on 256 CUs, so the
+    default path runs the 64-row kernel), here with K/V heads shared by
+    groups of query heads."""
     B, H, N, D = 1, 16, 2048, 64
     Q = _randn((B, H, N, D), 11)
     K = _randn((B, Hkv, N, D), 12)
@@ -56,7 +56,7 @@ def test_gqa_causal_row_block_pairs(fa, dev, Hkv):
     g = H // Hkv
     Or, Lr = naive_attention(half_cast(Q), np.repeat(half_cast(K), g, axis=1),
                              np.repeat(half_cast(V), g, axis=1), causal=True)
-    _check(O, L, Or, Lr, tag=f"GQA pairs H{H} Hkv{Hkv} N{N} D{D} causal")
+    _check(O, L, Or, Lr, tag=f"GQA causal H{H} Hkv{Hkv} N{N} D{D}")
 
 
 def test_gqa_with_all_heads_equals_mha(fa, dev):
