@@ -42,6 +42,14 @@ Pinning status (each function is checked in tests/test_oracle.py):
 * naive_attention_backward (tests/test_backward.py:20-46): float64 central
   finite differences of sum(naive_attention(Q, K, V) * dO) in every input
   element, causal and not, on tiny inputs.
+* fp16_p_forward (the reference kernel's fp16 rounding of P and O,
+  cuda/flash_attn_fa3_db_full.cu:266-293, :330-339): with round_p=False its O
+  equals naive_attention's rounded to fp16 (the running-max bookkeeping,
+  lazy or per tile, is exact algebra); with round_p=True it equals a
+  pure-Python loop that rounds each P to fp16 on tiny inputs, whatever m
+  sequence is used the result is a convex combination of V rows, and planted
+  mistakes (normalising by the rounded sum, dropping the rescale of O) move
+  it away from the loop.
 """
 from __future__ import annotations
 
@@ -323,6 +331,124 @@ def lse_combine(Os, Ls):
 # ----------------------------------------------------------------------------
 # Seeded synthetic inputs (the BASELINE configs)
 # ----------------------------------------------------------------------------
+
+def fp16_p_forward(Q, K, V, causal: bool = False, round_p: bool = True, lazy_max: bool = True,
+                   rows: int = 128, tile_groups: int = 2, norm_rounded: bool = False):
+    """O (fp16-rounded, as float64) and L of one head with the kernels' rounding.
+
+    The reference's fused forward rounds P = 2^(S log2e/sqrt(D) - m) to fp16
+    before the PV product (pack_half2, cuda/flash_attn_fa3_db_full.cu:286-293)
+    and normalises O by the row sum of the UNROUNDED exponentials (:266-284),
+    then rounds O to fp16 (:330-339). This function restates that arithmetic
+    on Q, K, V [N, D] (fp16 values), so the error a kernel with fp16 P and
+    fp16 O cannot avoid can be told apart from kernel error:
+
+    * scores in fp32 (float64 sums of the exact fp16 products, rounded once),
+      c = fl32(log2 e) / sqrt(D), x = fl32(s c - m), P32 = fl32(2^x);
+    * round_p: P16 = fp16(P32) feeds PV (else P32 itself: only O is rounded);
+    * the row sum l accumulates P32;
+    * lazy_max=True restates the HIP kernel's running-max rule instead of the
+      reference's per-tile maximum: rows advance in 64-key tiles, key tile t
+      belongs to tile group t mod ``tile_groups``, each (32-row wave, tile
+      group) keeps its own (m, l, O), and m is raised to the tile's row
+      maximum only when some lane's half-row tile sum (the 32 keys a lane
+      holds: keys k with (k mod 8) div 4 equal to the lane's half) exceeds
+      2^15 or is not finite, for every row of the wave at once; the groups
+      merge at the end with weights 2^(m_g - M). lazy_max=False raises m to
+      the running maximum on every tile (the reference's rule, :250-264).
+
+    norm_rounded=True normalises O by the sum of the rounded P instead (the
+    arithmetic of a kernel that sums the P it multiplies; L keeps the
+    unrounded sum), to cost that alternative.
+
+    Returns (O [N, D] float64 holding fp16 values, L [N] float64). Test
+    infrastructure: it is the yardstick for the fp16 format floor, never a
+    product path. ``rows`` is the workgroup's row block (128 for the kernel
+    the ragged configs run); only the tile grouping, not the block size,
+    changes the arithmetic.
+    """
+    Q = np.asarray(Q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    N, D = Q.shape
+    Nk = K.shape[0]
+    c = float(np.float32(np.float32(1.4426950408889634) * np.float32(1.0 / math.sqrt(D))))
+    S = (Q @ K.T).astype(np.float32).astype(np.float64)
+    keys = np.arange(Nk)
+    if causal:
+        S = np.where(keys[None, :] > np.arange(N)[:, None], -np.inf, S)
+    n_tiles = (Nk + 63) // 64
+    half = ((np.arange(64) % 8) // 4)[None, :]             # lane half of key k of a tile
+    waves = (N + 31) // 32
+    TG = tile_groups if lazy_max else 1
+    m = np.full((TG, N), -np.inf)
+    lh = np.zeros((TG, N, 2))                                # per lane-half sums
+    lr = np.zeros((TG, N))                                   # sum of the rounded P
+    O = np.zeros((TG, N, V.shape[1]))
+    for t in range(n_tiles):
+        g = t % TG
+        k0, k1 = 64 * t, min(64 * t + 64, Nk)
+        st = np.full((N, 64), -np.inf)
+        st[:, :k1 - k0] = S[:, k0:k1]
+        vt = np.zeros((64, V.shape[1]))
+        vt[:k1 - k0] = V[k0:k1]
+        tmax = st.max(axis=1) * c                           # row max of s c (fp32 value * c)
+        tmax = np.asarray(np.float32(tmax), np.float64)
+
+        def expo(mm):
+            ms = np.where(np.isfinite(mm), mm, 0.0) if not lazy_max else mm
+            with np.errstate(invalid="ignore"):
+                x = np.asarray(np.float32(st * c - ms[:, None]), np.float64)
+            x = np.where(np.isnan(x), np.nan, x)
+            with np.errstate(over="ignore"):
+                return np.asarray(np.float32(np.exp2(x)), np.float64)
+
+        if lazy_max:
+            P = expo(m[g])
+            hs = np.stack([np.where(half == h_, P, 0.0).sum(axis=1) for h_ in (0, 1)], axis=1)
+            bad = ~(hs <= 32768.0)                          # NaN and inf count as bad
+            wbad = np.zeros(waves * 32, bool)
+            wbad[:N] = bad.any(axis=1)
+            wbad = wbad.reshape(waves, 32).any(axis=1)
+            rescue = np.repeat(wbad, 32)[:N]
+            if rescue.any():
+                m_new = np.where(rescue, np.maximum(m[g], tmax), m[g])
+                with np.errstate(invalid="ignore"):
+                    alpha = np.where(m_new == m[g], 1.0, np.exp2(m[g] - m_new))
+                lh[g] *= alpha[:, None]
+                lr[g] *= alpha
+                O[g] *= alpha[:, None]
+                m[g] = m_new
+                msafe = np.where(np.isfinite(m[g]), m[g], 0.0)
+                P = expo(msafe)
+        else:
+            m_new = np.maximum(m[g], tmax)
+            with np.errstate(invalid="ignore"):
+                alpha = np.where(m_new == m[g], 1.0, np.exp2(m[g] - m_new))
+            lh[g] *= alpha[:, None]
+            lr[g] *= alpha
+            O[g] *= alpha[:, None]
+            m[g] = m_new
+            P = expo(np.where(np.isfinite(m[g]), m[g], 0.0))
+        P = np.where(np.isnan(P), 0.0, P)
+        lh[g, :, 0] += np.where(half == 0, P, 0.0).sum(axis=1)
+        lh[g, :, 1] += np.where(half == 1, P, 0.0).sum(axis=1)
+        Pv = P.astype(np.float16).astype(np.float64) if round_p else P
+        lr[g] += Pv.sum(axis=1)
+        O[g] += Pv @ vt
+    M = m.max(axis=0)
+    with np.errstate(invalid="ignore"):
+        a = np.where(m == M[None, :], 1.0, np.exp2(m - M[None, :]))
+    a = np.where(np.isnan(a), 0.0, a)
+    l = (lh.sum(axis=2) * a).sum(axis=0)
+    Ot = (O * a[:, :, None]).sum(axis=0)
+    ln = (lr * a).sum(axis=0) if norm_rounded else l
+    inv = np.where(ln > 0, 1.0 / np.where(ln > 0, ln, 1.0), 0.0)
+    O16 = (Ot * inv[:, None]).astype(np.float32).astype(np.float16).astype(np.float64)
+    with np.errstate(divide="ignore"):
+        L = np.where(l > 0, (M + np.log2(np.where(l > 0, l, 1.0))) * LN2, -np.inf)
+    return O16, L
+
 
 def randn_f16(rng: np.random.Generator, shape, amp: float = 1.0) -> np.ndarray:
     """N(0, amp^2) samples rounded to fp16 (the GPU sees exactly these bits)."""

@@ -47,3 +47,16 @@ def capi():
 def dev():
     import torch
     return torch.device("cuda:0")
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Print the forward error envelope the GPU tests measured (tests/errlog.py)."""
+    try:
+        import errlog
+    except ImportError:   # pragma: no cover
+        return
+    lines = errlog.summary_lines()
+    if lines:
+        terminalreporter.section("forward error envelope")
+        for line in lines:
+            terminalreporter.write_line(line)

@@ -508,3 +508,95 @@ def test_bench_decode_metadata_matches_the_oracle_generator():
         a = bench.decode_meta(B=32, seed=seed)
         b = orc.make_decode_meta(B=32, seed=seed)
         assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]) and a[2] == b[2]
+
+
+# --- fp16_p_forward: the reference kernel's fp16 rounding of P and O ---------
+
+def _fp16(x):
+    return np.asarray(x, np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+
+
+def _fp16_p_loop(q, k, v, causal, normalise_by_rounded=False, rescale_o=True):
+    """Pure-Python restatement, row by row, of the reference kernel's loop
+    (cuda/flash_attn_fa3_db_full.cu:250-293, :330-339): 64-key tiles, m raised
+    to the running max every tile, P = fl32(2^(fl32(s c - m))) summed unrounded
+    into l and rounded to fp16 for O += P V, O = fp16(O / l). The keyword
+    arguments plant the mistakes the pinning test must see."""
+    N, D = q.shape
+    c = float(np.float32(np.float32(1.4426950408889634) * np.float32(1.0 / math.sqrt(D))))
+    out = np.zeros((N, v.shape[1]))
+    for i in range(N):
+        s = [float(np.float32(sum(float(q[i, d]) * float(k[j, d]) for d in range(D))))
+             for j in range(k.shape[0])]
+        if causal:
+            s = [x if j <= i else -math.inf for j, x in enumerate(s)]
+        m, l, lr, o = -math.inf, 0.0, 0.0, np.zeros(v.shape[1])
+        for t0 in range(0, len(s), 64):
+            tile = s[t0:t0 + 64]
+            tm = float(np.float32(max(tile) * c)) if max(tile) > -math.inf else -math.inf
+            mn = max(m, tm)
+            alpha = 1.0 if mn == m else 2.0 ** (m - mn)
+            l *= alpha
+            lr *= alpha
+            if rescale_o:
+                o = o * alpha
+            ms = mn if mn > -math.inf else 0.0
+            for j, x in enumerate(tile):
+                p = float(np.float32(2.0 ** float(np.float32(x * c - ms)))) if x > -math.inf else 0.0
+                p16 = float(_fp16(p))
+                l += p
+                lr += p16
+                o = o + p16 * v[t0 + j]
+            m = mn
+        out[i] = _fp16(o / (lr if normalise_by_rounded else l))
+    return out
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lazy", [True, False])
+def test_fp16_p_forward_without_p_rounding_is_naive_attention(causal, lazy):
+    """round_p=False: the running-max bookkeeping (lazy or per tile) is exact
+    algebra, so O is the naive result rounded to fp16 (within one fp16 ulp,
+    where the two round a value near a rounding boundary differently, plus
+    fp32 noise of the terms where a row's terms cancel) and L is the naive L."""
+    for N, amp in ((1, 1.0), (63, 1.0), (200, 3.0), (333, 1.0)):
+        Q, K, V = (orc.half_cast(x)[0, 0] for x in orc.make_fwd_inputs(1, 1, N, 64, seed=N, amp=amp))
+        Or, Lr = orc.naive_attention(Q[None, None], K[None, None], V[None, None], causal=causal,
+                                     dtype=np.float64)
+        O, L = orc.fp16_p_forward(Q, K, V, causal=causal, round_p=False, lazy_max=lazy)
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(Or[0, 0]), 2.0 ** -14))) - 10)
+        assert (np.abs(O - Or[0, 0]) <= ulp + 1e-6 * np.abs(V).max()).all(), (N, amp)
+        assert np.abs(L - Lr[0, 0]).max() <= 1e-5 * max(1.0, np.abs(Lr).max()), (N, amp)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp16_p_forward_matches_the_loop_and_catches_planted_mistakes(causal):
+    """With the reference's per-tile max (lazy_max=False), fp16_p_forward is
+    the row-by-row loop above on peaky inputs (std-3 Q and K: a few keys carry
+    each row); normalising by the rounded sum, or dropping O's rescale, moves
+    the loop's result away from it."""
+    N, D = 150, 16
+    Q, K, V = (orc.half_cast(x)[0, 0] for x in orc.make_fwd_inputs(1, 1, N, D, seed=5, amp=3.0))
+    O, _ = orc.fp16_p_forward(Q, K, V, causal=causal, lazy_max=False)
+    want = _fp16_p_loop(Q, K, V, causal)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -14))) - 10)
+    assert (np.abs(O - want) <= ulp).all()
+    assert np.abs(O - want).max() <= 1e-3
+    Or_, _ = orc.fp16_p_forward(Q, K, V, causal=causal, lazy_max=False, norm_rounded=True)
+    want_r = _fp16_p_loop(Q, K, V, causal, normalise_by_rounded=True)
+    assert (np.abs(Or_ - want_r) <= ulp).all()
+    planted = [want_r, _fp16_p_loop(Q, K, V, causal, rescale_o=False)]
+    for bad in planted:
+        assert np.abs(bad - O).max() > 2 * np.abs(want - O).max() + 1e-6
+
+
+def test_fp16_p_forward_is_a_convex_combination():
+    """Whatever the running-max rule, every O element lies within the range of
+    its V column (up to P's and O's rounding)."""
+    N, D = 500, 64
+    Q, K, V = (orc.half_cast(x)[0, 0] for x in orc.make_fwd_inputs(1, 1, N, D, seed=9, amp=3.0))
+    for lazy in (True, False):
+        O, _ = orc.fp16_p_forward(Q, K, V, lazy_max=lazy)
+        lo, hi = V.min(axis=0), V.max(axis=0)
+        slack = 2.0 ** -10 * np.abs(V).max(axis=0)
+        assert (O >= lo - slack).all() and (O <= hi + slack).all()
