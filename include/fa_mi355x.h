@@ -297,7 +297,11 @@ int fa_decode_paged_gqa_f16(const void* q, const void* k_pool, const void* v_poo
  * split partials go to a static device array of FA_DECODE_SCRATCH_FLOATS
  * floats that the library holds on each GPU it runs on until the process
  * ends (its address is resolved once per device, on that device's first
- * call). Needs B*H*num_splits*(D+1) <= FA_DECODE_SCRATCH_FLOATS, else
+ * call: make that first call outside HIP graph capture; later calls record
+ * only kernel launches and can be captured and replayed, which
+ * tests/test_zz_no_alloc.py checks bit for bit against
+ * fa_decode_paged_gqa_f16). Needs B*H*num_splits*(D+1) <=
+ * FA_DECODE_SCRATCH_FLOATS, else
  * FA_ERR_SCRATCH_SIZE (B = 32, H = 32, D = 128, 16 splits uses half). Makes
  * no hipMalloc/hipFree or other allocating call. Nothing in the array has to
  * start at zero (every partial a call reads, that call wrote). All calls on

@@ -222,13 +222,16 @@ def test_config5_full_size(fa, dev):
 
 @pytest.mark.parametrize("D,Hkv,dtype", [(64, 4, torch.float16), (128, 4, torch.float16),
                                          (64, 1, torch.float16), (128, 2, torch.float16),
-                                         (128, 4, torch.bfloat16)])
+                                         (128, 1, torch.float16), (128, 4, torch.bfloat16),
+                                         (128, 1, torch.bfloat16)])
 def test_garbage_past_context_is_ignored(fa, dev, D, Hkv, dtype):
     """Slots past ctx in a sequence's last page hold whatever the pool held
     (pools come from torch.empty; kv_append writes only up to the context).
     NaN and Inf there must not reach O or L: the result equals the oracle's,
     which gathers only the first ctx tokens, for the one-head-per-workgroup
-    kernel (Hkv = H) and the grouped kernels (Hkv < H)."""
+    kernel (Hkv = H) and the grouped kernels (Hkv < H; Hkv = 1 at D = 128 is
+    the four-head kernel whose lanes hold two tokens of a page, t and t + 8,
+    so the slots past ctx reach both of a lane's tokens)."""
     H = 4
     ctx = [1, 15, 17, 40, 300, 33]
     q, kp, vp, table, ctxa = _small(21 + D + Hkv, B=len(ctx), H=Hkv, D=D, ctx=ctx, extra_pages=1)

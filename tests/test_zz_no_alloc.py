@@ -5,7 +5,8 @@ library's static device array instead of a caller workspace, so its O and L
 must equal that entry point's bit for bit. Both are called through the C ABI
 (ctypes, raw device pointers). Two calls in a row, the second smaller, show
 that nothing left in the array by one call leaks into the next; a call near
-the array's limit touches its far end. O and L are also held to the oracle
+the array's limit touches its far end; a call captured in a HIP graph replays
+correctly after the device's first call. O and L are also held to the oracle
 (oracle/naive.py: decode_attention) at the decode bars: O max-abs <= 2e-3,
 L relative <= 1e-4.
 """
@@ -113,3 +114,41 @@ def test_rejects_beyond_the_limit(capi, dev):
     assert b"FA_DECODE_SCRATCH_FLOATS" in lib.fa_status_str(st)
     torch.cuda.synchronize()
     assert torch.count_nonzero(o) == 0
+
+
+def test_captured_in_a_hip_graph(capi, dev):
+    """After one call outside capture (which resolves the array's address on
+    this device), a call captured in a HIP graph replays correctly: every
+    replay, with eager work and synchronisations between them and new q
+    values copied into the captured buffer, equals fa_decode_paged_gqa_f16 on
+    the same inputs bit for bit. The entry point records only kernels (no
+    memset node, no allocation)."""
+    lib = capi.load()
+    B, H, Hkv, D, S = 5, 8, 2, 128, 6
+    q, kp, vp, table, ctx = _case(76, B=B, H=H, Hkv=Hkv, D=D, ctx=[1, 40, 700, 16, 2100])
+    tq, tk, tv, tt, tc = _to(dev, q, kp, vp, table, ctx)
+    head = lambda: (tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tt.data_ptr(), tc.data_ptr(),  # noqa: E731
+                    B, H, Hkv, D, 16, tt.shape[1], tk.shape[0], S)
+    o = torch.zeros(B, H, D, device=dev, dtype=torch.float16)
+    lse = torch.zeros(B, H, device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.fa_decode_paged_noalloc_f16(*head(), o.data_ptr(), lse.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream().cuda_stream
+        st = lib.fa_decode_paged_noalloc_f16(*head(), o.data_ptr(), lse.data_ptr(), cs)
+    assert st == 0, lib.fa_status_str(st)
+    rng = np.random.default_rng(77)
+    for rep in range(4):
+        new_q = rng.standard_normal((B, H, D)).astype(np.float16)
+        tq.copy_(torch.from_numpy(new_q).to(dev))
+        o.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        o_ws, l_ws = _run(lib, lib.fa_decode_paged_gqa_f16, tq, tk, tv, tt, tc, Hkv, S, stream,
+                          workspace=True)
+        assert torch.equal(o, o_ws), f"replay {rep}: O differs"
+        assert torch.equal(lse, l_ws), f"replay {rep}: L differs"
+        _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
