@@ -151,14 +151,15 @@ def decode_meta(B=32, ctx_lo=512, ctx_hi=32768, page_size=16, seed=5):
 
 
 def bench_read_ceiling(fa, torch, dev, reps=5, iters=5):
-    """HBM read rate of a plain streaming kernel (fa_probe_read_bw: 16-byte
-    loads, 8 in flight per thread) over 4 GiB, at several grid sizes: the
-    practical ceiling the decode's split pass is compared with."""
+    """HBM read rate of a plain streaming kernel (fa_probe_read_bw: one
+    contiguous chunk per workgroup, 16-byte non-temporal loads, 8 in flight
+    per thread) over 4 GiB, at several grid sizes: the practical ceiling the
+    decode's split pass is compared with."""
     nbytes = 4 * 1024 ** 3
     x = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     res = {}
-    for blocks in (4096, 8192, 16384):
+    for blocks in (2048, 4096, 8192):
         ms = median_of(lambda: fa.probe.probe_read_bw(x, sink, blocks), reps, 2, iters, torch)
         res[f"blocks_{blocks}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
     del x

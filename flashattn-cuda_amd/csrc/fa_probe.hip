@@ -198,25 +198,34 @@ extern "C" int fa_probe_chain(const void* q, const void* k, const void* v, float
 }
 
 namespace fa {
-// Streaming read of `n` 16-byte vectors, grid-stride with 8 loads in flight
-// per thread, folded into one word per lane (written only on a 2^-32
-// chance, so the loads stay and the stores do not count): the HBM read rate
-// a plain kernel reaches, the ceiling the paged decode is compared with.
+// Streaming read of `n` 16-byte vectors folded into one word per lane
+// (written only on a 2^-32 chance, so the loads stay and the stores do not
+// count): the HBM read rate a plain kernel reaches, the ceiling the paged
+// decode is compared with.
 __global__ void __launch_bounds__(256)
 probe_read_kernel(const uint4* __restrict__ p, size_t n, uint32_t* __restrict__ sink) {
-  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t stride = (size_t)gridDim.x * 256;
+  // Each workgroup streams one contiguous chunk of the buffer (the last one
+  // also the remainder), 8 loads of 16 bytes per thread in flight, with the
+  // non-temporal hint: measured on MI355X over 4 GiB, 7.0-7.1 TB/s, against
+  // 6.2-6.3 TB/s for the same loads without the hint and 5.7-6.2 TB/s for a
+  // grid-stride loop whose 8 loads lie a grid apart.
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const size_t per = n / gridDim.x;
+  const size_t begin = (size_t)blockIdx.x * per;
+  const size_t end = blockIdx.x + 1 == gridDim.x ? n : begin + per;
+  const u4* q = reinterpret_cast<const u4*>(p);
   uint32_t acc = 0;
-  for (; i + 7 * stride < n; i += 8 * stride) {
-    uint4 v[8];
+  size_t i = begin + threadIdx.x;
+  for (; i + 7 * 256 < end; i += 8 * 256) {
+    u4 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = p[i + u * stride];
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(q + i + u * 256);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
   }
-  for (; i < n; i += stride) {
-    const uint4 v = p[i];
-    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  for (; i < end; i += 256) {
+    const u4 v = __builtin_nontemporal_load(q + i);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;
 }

@@ -83,11 +83,11 @@ int fa_probe_splitkv_plan_cus(int64_t B, int64_t H, int64_t N, int64_t D, int ca
 int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal);
 
 /* Streams `bytes` (a multiple of 16, 16-byte aligned) from device memory at p
- * with `blocks` workgroups of 256 threads, 16-byte loads, 8 in flight per
- * thread: the read bandwidth a plain kernel reaches on this device, the
- * ceiling the paged decode's split pass is measured against. sink: one
- * device uint32, written only on a 2^-32 chance. 1: NULL argument, 2: bad
- * size, alignment or grid. */
+ * with `blocks` workgroups of 256 threads, each over one contiguous chunk,
+ * 16-byte non-temporal loads, 8 in flight per thread: the read bandwidth a
+ * plain kernel reaches on this device, the ceiling the paged decode's split
+ * pass is measured against. sink: one device uint32, written only on a
+ * 2^-32 chance. 1: NULL argument, 2: bad size, alignment or grid. */
 int fa_probe_read_bw(const void* p, int64_t bytes, int blocks, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus

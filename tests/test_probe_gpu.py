@@ -101,3 +101,9 @@ def test_read_bandwidth_probe_runs(fa, dev):
         fa.probe.probe_read_bw(x, sink, blocks)
     torch.cuda.synchronize()
     assert sink.item() == 0
+    # The loads read the data: one 16-byte vector whose words fold to the
+    # trigger value, in the chunk of the last of 64 workgroups, sets the sink.
+    x.view(-1, 4)[-1, 0] = 0x9e3779b9 - (1 << 32)
+    fa.probe.probe_read_bw(x, sink, 64)
+    torch.cuda.synchronize()
+    assert sink.item() == 0x9e3779b9 - (1 << 32)
