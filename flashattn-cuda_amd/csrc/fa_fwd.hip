@@ -601,11 +601,16 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) kl[kk] = lds_lane_base(kt + koffs[kk]);
     const lds_cp vl = lds_lane_base(vt + voff_l);
-    // MFMA m is PV i or QK i: with PV, even m = PV m / 2 and odd m = QK
-    // m / 2; without PV, QK m. QK i: block i % NB, k-step i / NB. PV i:
-    // k-step i / DB, d-block i % DB: V block i.
-    auto is_pv = [](int m) { return PV && (m & 1) == 0; };
-    auto idx = [](int m) { return PV ? m >> 1 : m; };
+    // MFMA m is PV i or QK i. With PV, in groups of four: QK 2j and 2j + 1
+    // (the two 32-key blocks of k-step j, one Q^T operand), then PV 2j and
+    // 2j + 1 (two d-blocks of one P^T operand), so consecutive MFMAs share
+    // their B operand (1.6 % faster at the headline than alternating PV and
+    // QK, same results: each accumulator still sums its k-steps in order);
+    // every accumulator is reused four MFMAs later. Without PV, QK m. QK i:
+    // block i % NB, k-step i / NB. PV i: k-step i / DB, d-block i % DB: V
+    // block i.
+    auto is_pv = [](int m) { return PV && (m & 3) >= 2; };
+    auto idx = [](int m) { return PV ? 2 * (m >> 2) + (m & 1) : m; };
     auto fetch = [&](int m) -> f16x8 {
       const int i = idx(m);
       if (is_pv(m)) return vblk_frag(vl + i * 1024);
