@@ -560,7 +560,10 @@ fa_fwd_pp_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
   // Prologue: the waves share the copies of K tiles 0 .. RING - TG/2 - 1 and
   // V tiles 0 .. RING - 3 TG/2 - 1 (those read before the first M-phase
   // copies land), 1 KiB block by block. (Waiting only for the K tiles of
-  // step 0 here and for the rest during phase 0 measured 1-2% slower.)
+  // step 0 here and for the rest during phase 0 measured 1-2% slower; so did,
+  // by 3-6 % at every non-causal shape, group 1 copying and awaiting K tiles
+  // 0 .. TG-1 while group 0 copies the rest and awaits them at the end of its
+  // phase-0 softmax.)
   {
     constexpr int NK = RING - TG / 2, NV = RING - 3 * TG / 2;
     constexpr int ITEMS = (NK + NV) * BLOCKS;
