@@ -229,7 +229,6 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
   const int bh = logical / num_kb;
   const int kb = logical - bh * num_kb;
   const int k0 = kb * kBlk;
-  const int key = k0 + 32 * kw + (lane & 31);
 
   const HeadView hv = head_view<D>(geo, bh);
   const int N = hv.n;
@@ -305,9 +304,13 @@ __device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* 
     }
     if (edge) {   // rows past N, and (causal) keys after the row
       // Register r holds query base + 8 (r/4) + r%4: compare that constant
-      // offset against two per-lane limits.
-      const int base = qt0 + 32 * qb + 4 * hi;
-      const int lim_n = N - base, lim_k = key - base;
+      // offset against two per-lane limits. The lane id is read here again
+      // (volatile, so the key index is not held across the loop: at D = 128
+      // that register is one of those the causal instance would spill).
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      const int base = qt0 + 32 * qb + 4 * (ln >> 5);
+      const int lim_n = N - base, lim_k = k0 + 32 * kw + (ln & 31) - base;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int ro = 8 * (r >> 2) + (r & 3);
@@ -1015,10 +1018,6 @@ fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
   reinterpret_cast<f32x4*>(out)[i4] = acc;
 }
 
-// Units per half, per CU, below which the D = 128 causal backward runs
-// fused: two (measured crossover on MI355X's 256 CUs, see launch_bwd).
-constexpr int kFuseUnitsPerCuD128 = 2;
-
 // Wave groups per workgroup: two (the second group takes the other half of
 // every tile, so the grid stays one workgroup per 128 rows and the SIMDs get
 // a second wave to overlap). At D = 128 the dK/dV body then fills the 256
@@ -1039,7 +1038,7 @@ template <int D, bool CAUSAL, bool BF16>
 static hipError_t launch_bwd(const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, float* dq, float* dk, float* dv,
                              float* ws, const Geom& geo, int64_t units, int64_t rows,
-                             int64_t out_heads, int64_t head_rows, int cus, hipStream_t s) {
+                             int64_t out_heads, int64_t head_rows, hipStream_t s) {
   const float scale = (float)(1.0 / sqrt((double)D));
   const float c = scale * kLog2e;
   const f16* Q = (const f16*)q;
@@ -1060,20 +1059,18 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   const int total = (int)(units * nb);
   constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
   bool launched = false;
-  // One launch where it pays (measured): at D = 64 always; at D = 128 only
-  // for causal heads with fewer units per half than two per CU, where one
-  // wave of workgroups cannot even out the triangle (B1 H8 N4096: 0.237 ->
-  // 0.165 ms). From 512 units on the two launches win (B2 H8 N4096 causal
-  // 307 -> 304 us, B4 H16 N4096 causal 1267 -> 1237 us), and so they do for
-  // non-causal heads (B4 H16 N4096: 2.36 vs 2.50 ms), whose units are all
-  // the same length. (The fused D = 128 body also needs 4 VGPRs more than
-  // the two budgets allow and spills them; the separate kernels do not.)
+  // One launch where it pays (measured): at D = 64 always; at D = 128 for
+  // causal heads, where a short wave of workgroups cannot even out the
+  // triangle on its own (B1 H8 N4096: 0.237 -> 0.165 ms) and larger grids
+  // run the same in one launch as in two (B2 H8 N4096 303.2 / 301.1 us,
+  // B4 H8 600.8 / 597.2 us, B4 H16 1237.2 / 1237.9 us, B1 H16 N8192
+  // 1082.9 / 1081.2 us; same gradients bit for bit). Non-causal D = 128
+  // heads, whose units are all the same length, keep the two launches
+  // (B4 H16 N4096: 2.36 vs 2.50 ms).
   if constexpr (GK == 2 && GQ == 2 && (D == 64 || CAUSAL)) {
-    if (D == 64 || total < kFuseUnitsPerCuD128 * cus) {
-      hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
-                         s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
-      launched = true;
-    }
+    hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
+                       s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
+    launched = true;
   }
   if (!launched) {
     hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
@@ -1120,17 +1117,15 @@ static int bwd_run(const void* q, const void* k, const void* v, const void* o, c
                    const Geom& geo_in, int64_t units, int64_t rows, int64_t out_heads,
                    int64_t head_rows, int64_t D, int causal, void* stream) {
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Topology topo = stream_topology(s);
   Geom geo = geo_in;
-  geo.nxcd = topo.xcds;
-  const int cus = topo.cus;
+  geo.nxcd = stream_topology(s).xcds;
   hipError_t e;
   if (D == 64) {
-    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s)
-               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s);
+    e = causal ? launch_bwd<64, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s)
+               : launch_bwd<64, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s);
   } else {
-    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s)
-               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, cus, s);
+    e = causal ? launch_bwd<128, true, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s)
+               : launch_bwd<128, false, BF16>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, units, rows, out_heads, head_rows, s);
   }
   return e == hipSuccess ? FA_OK : -(int)e;
 }
