@@ -158,10 +158,10 @@ def test_headline_shape(fa, dev, D, causal):
     np.testing.assert_allclose(dK.sum(axis=2), 0, atol=2e-3 * scale)
 
 
-def test_causal_d128_two_launch_grid(fa, dev):
-    """D = 128 causal with 512 units per half (B2 H8 N4096): the grid size at
-    which the backward runs the separate dK/dV and dQ kernels instead of the
-    fused launch. Two heads against the oracle, every head through the
+def test_causal_d128_two_rounds(fa, dev):
+    """D = 128 causal with 512 units per half (B2 H8 N4096): the fused launch
+    over more workgroups than one round of CUs, so units of both roles start
+    as others finish. Two heads against the oracle, every head through the
     identities of test_headline_shape."""
     B, H, N, D = 2, 8, 4096, 128
     Q, K, V, G = _randn(B, H, N, D, 77)
