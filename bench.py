@@ -153,8 +153,9 @@ def decode_meta(B=32, ctx_lo=512, ctx_hi=32768, page_size=16, seed=5):
 def bench_read_ceiling(fa, torch, dev, reps=5, iters=5):
     """HBM read rate of a plain streaming kernel (fa_probe_read_bw: one
     contiguous chunk per workgroup, 16-byte non-temporal loads, 8 in flight
-    per thread) over 4 GiB, at several grid sizes: the practical ceiling the
-    decode's split pass is compared with."""
+    per thread) over 4 GiB, at several grid sizes, and of a gather of random
+    4 KiB pages (fa_probe_gather_bw): the practical ceilings the decode's
+    split pass is compared with."""
     nbytes = 4 * 1024 ** 3
     x = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -166,6 +167,23 @@ def bench_read_ceiling(fa, torch, dev, reps=5, iters=5):
     torch.cuda.empty_cache()
     res["best_GBps"] = max(v for k, v in res.items())
     res["bytes"] = nbytes
+    # The decode's own read pattern (fa_probe_gather_bw): 4 KiB pages of two
+    # 2 GiB pools through a random permutation, 65 pages per workgroup (a
+    # config-5 split), with and without the non-temporal hint.
+    pages = 512 * 1024
+    kx = torch.zeros(pages * 1024, dtype=torch.int32, device=dev)
+    vx = torch.zeros(pages * 1024, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(5)
+    table = torch.randperm(pages, generator=g).to(torch.int32).to(dev)
+    gather = {}
+    for nt in (True, False):
+        ms = median_of(lambda: fa.probe.probe_gather_bw(kx, vx, table, sink, 65, nt), reps, 2,
+                       iters, torch)
+        gather["nontemporal_GBps" if nt else "plain_GBps"] = round(2 * pages * 4096 / (ms * 1e-3) / 1e9, 1)
+    gather["bytes"] = 2 * pages * 4096
+    res["gather_4KiB_pages"] = gather
+    del kx, vx, table
+    torch.cuda.empty_cache()
     return res
 
 

@@ -63,6 +63,7 @@ SIGNATURES = {
     "fa_probe_choose_variant": (C.c_int, [_i64, C.c_int, _i64, _i64, C.c_int]),
     "fa_probe_splitkv_plan_cus": (C.c_int, [_i64] * 4 + [C.c_int, C.c_int]),
     "fa_probe_read_bw": (C.c_int, [_vp, _i64, C.c_int, _vp, _vp]),
+    "fa_probe_gather_bw": (C.c_int, [_vp, _vp, _vp, _i64, C.c_int, C.c_int, _vp, _vp]),
 }
 
 DECODE_SCRATCH_FLOATS = 1 << 22   # FA_DECODE_SCRATCH_FLOATS

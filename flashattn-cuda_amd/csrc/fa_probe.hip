@@ -229,7 +229,58 @@ probe_read_kernel(const uint4* __restrict__ p, size_t n, uint32_t* __restrict__ 
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;
 }
+
+// Gather read of 4 KiB pages of two pools through a table (the paged
+// decode's access pattern without its arithmetic): lane l of a wave reads
+// bytes 16 l .. 16 l + 15 of each 1 KiB quarter of the page, four loads per
+// pool and page, one page per wave in flight.
+template <bool NT>
+__global__ void __launch_bounds__(256)
+probe_gather_kernel(const uint4* __restrict__ k, const uint4* __restrict__ v,
+                    const int32_t* __restrict__ table, int64_t pages, int per,
+                    uint32_t* __restrict__ sink) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t first = (int64_t)blockIdx.x * per;
+  const int n = (int)min((int64_t)per, pages - first);
+  const u4* kq = reinterpret_cast<const u4*>(k);
+  const u4* vq = reinterpret_cast<const u4*>(v);
+  uint32_t acc = 0;
+  for (int i = wave; i < n; i += 4) {
+    const int64_t pid = min(max((int64_t)table[first + i], (int64_t)0), pages - 1);
+    const size_t base = (size_t)pid * 256 + lane;   // 256 16-byte vectors per page
+    u4 x[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = NT ? __builtin_nontemporal_load(kq + base + 64 * j) : kq[base + 64 * j];
+      x[4 + j] = NT ? __builtin_nontemporal_load(vq + base + 64 * j) : vq[base + 64 * j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
 }  // namespace fa
+
+extern "C" int fa_probe_gather_bw(const void* k, const void* v, const int32_t* table,
+                                  int64_t pages, int pages_per_wg, int nontemporal,
+                                  uint32_t* sink, void* stream) {
+  if (!k || !v || !table || !sink) return 1;
+  if (pages < 1 || pages_per_wg < 1 || ((reinterpret_cast<uintptr_t>(k) |
+                                         reinterpret_cast<uintptr_t>(v)) & 15u))
+    return 2;
+  const int64_t wgs = (pages + pages_per_wg - 1) / pages_per_wg;
+  if (wgs > (int64_t(1) << 31) - 1) return 2;
+  if (nontemporal)
+    hipLaunchKernelGGL(fa::probe_gather_kernel<true>, dim3((unsigned)wgs), dim3(256), 0,
+                       (hipStream_t)stream, (const uint4*)k, (const uint4*)v, table, pages,
+                       pages_per_wg, sink);
+  else
+    hipLaunchKernelGGL(fa::probe_gather_kernel<false>, dim3((unsigned)wgs), dim3(256), 0,
+                       (hipStream_t)stream, (const uint4*)k, (const uint4*)v, table, pages,
+                       pages_per_wg, sink);
+  return finish();
+}
 
 extern "C" int fa_probe_read_bw(const void* p, int64_t bytes, int blocks, uint32_t* sink,
                                 void* stream) {

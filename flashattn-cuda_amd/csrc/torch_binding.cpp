@@ -531,6 +531,28 @@ void probe_read_bw(torch::Tensor x, torch::Tensor sink, int64_t blocks) {
                "fa_probe_read_bw");
 }
 
+// One gather read of the 4 KiB pages of k and v (contiguous CUDA tensors of
+// equal size, a multiple of 4 KiB) in the order of table (int32, CUDA): the
+// paged decode's read pattern without its arithmetic.
+void probe_gather_bw(torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor sink,
+                     int64_t pages_per_wg, bool nontemporal) {
+  TORCH_CHECK(k.is_cuda() && v.is_cuda() && k.is_contiguous() && v.is_contiguous(),
+              "k and v must be contiguous CUDA tensors");
+  const int64_t bytes = k.numel() * (int64_t)k.element_size();
+  TORCH_CHECK(bytes == v.numel() * (int64_t)v.element_size() && bytes % 4096 == 0,
+              "k and v must hold the same whole number of 4 KiB pages");
+  TORCH_CHECK(table.is_cuda() && table.scalar_type() == torch::kInt && table.is_contiguous() &&
+                  table.numel() == bytes / 4096,
+              "table must be a contiguous CUDA int32 tensor of one entry per page");
+  TORCH_CHECK(sink.is_cuda() && sink.scalar_type() == torch::kInt && sink.numel() >= 1,
+              "sink must be a CUDA int32 tensor");
+  check_status(fa_probe_gather_bw(k.data_ptr(), v.data_ptr(), table.data_ptr<int>(), bytes / 4096,
+                                  (int)pages_per_wg, nontemporal ? 1 : 0,
+                                  reinterpret_cast<uint32_t*>(sink.data_ptr<int>()),
+                                  current_stream(k)),
+               "fa_probe_gather_bw");
+}
+
 torch::Tensor probe_chain(torch::Tensor q, torch::Tensor k, torch::Tensor v) {
   TORCH_CHECK(q.is_cuda() && q.dim() == 2 && q.size(0) == 32 && q.scalar_type() == torch::kHalf);
   const int64_t D = q.size(1);
@@ -585,6 +607,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("probe_frags", &probe_frags);
   m.def("probe_chain", &probe_chain);
   m.def("probe_read_bw", &probe_read_bw, py::arg("x"), py::arg("sink"), py::arg("blocks"));
+  m.def("probe_gather_bw", &probe_gather_bw, py::arg("k"), py::arg("v"), py::arg("table"),
+        py::arg("sink"), py::arg("pages_per_wg"), py::arg("nontemporal"));
   m.def("probe_fwd_variant", &probe_fwd_variant, py::arg("Q"), py::arg("K"), py::arg("V"),
         py::arg("causal") = false, py::arg("variant") = 12, py::arg("want_L") = true);
   m.def("probe_fwd_variants", &probe_fwd_variants);

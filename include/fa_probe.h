@@ -12,14 +12,14 @@
  * fa_abi_version): 2 added the causal argument of fa_probe_fwd_variants;
  * 3 removed variant 418 and added fa_probe_choose_variant and
  * fa_probe_splitkv_plan_cus (the kernel and split choices for a given
- * compute-unit count, without a device).
+ * compute-unit count, without a device); 4 added fa_probe_gather_bw.
  */
 #ifndef FA_PROBE_H
 #define FA_PROBE_H
 
 #include <stdint.h>
 
-#define FA_PROBE_VERSION 3
+#define FA_PROBE_VERSION 4
 
 #ifdef __cplusplus
 extern "C" {
@@ -89,6 +89,17 @@ int fa_probe_fwd_variants(int* out, int max_out, int64_t D, int causal);
  * pass is measured against. sink: one device uint32, written only on a
  * 2^-32 chance. 1: NULL argument, 2: bad size, alignment or grid. */
 int fa_probe_read_bw(const void* p, int64_t bytes, int blocks, uint32_t* sink, void* stream);
+
+/* Reads `pages` 4 KiB pages from each of two pools (k, v: pages * 4096
+ * bytes each, 16-byte aligned) in the order of `table` (int32 page ids,
+ * clamped into [0, pages)), the access pattern of the paged decode: one
+ * workgroup of 4 waves per `pages_per_wg` consecutive table entries, wave w
+ * taking entries w, w + 4, ...; each load instruction reads 1 KiB of a page
+ * contiguously, with the non-temporal hint when `nontemporal` is non-zero.
+ * The ceiling of the decode's split pass for a given table. sink as above.
+ * 1: NULL argument, 2: bad size, alignment or grid. */
+int fa_probe_gather_bw(const void* k, const void* v, const int32_t* table, int64_t pages,
+                       int pages_per_wg, int nontemporal, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -310,7 +310,8 @@ def test_bf16_decode_and_page_writer_reject_before_touching_the_device(capi):
 
 
 def test_read_probe_rejects_before_touching_the_device(capi):
-    """fa_probe_read_bw checks its pointers, size, alignment and grid first."""
+    """fa_probe_read_bw and fa_probe_gather_bw check their pointers, sizes,
+    alignment and grid first."""
     lib = capi.load()
     assert lib.fa_probe_read_bw(None, 1024, 8, A, None) == 1
     assert lib.fa_probe_read_bw(A, 1024, 8, None, None) == 1
@@ -318,6 +319,13 @@ def test_read_probe_rejects_before_touching_the_device(capi):
     assert lib.fa_probe_read_bw(A, 0, 8, A, None) == 2
     assert lib.fa_probe_read_bw(A, 1024, 0, A, None) == 2     # no workgroups
     assert lib.fa_probe_read_bw(A + 8, 1024, 8, A, None) == 2  # 8-byte aligned only
+    g = lib.fa_probe_gather_bw   # (k, v, table, pages, pages_per_wg, nontemporal, sink, stream)
+    assert g(None, A, A, 16, 4, 1, A, None) == 1
+    assert g(A, A, None, 16, 4, 1, A, None) == 1
+    assert g(A, A, A, 16, 4, 1, None, None) == 1
+    assert g(A, A, A, 0, 4, 1, A, None) == 2          # no pages
+    assert g(A, A, A, 16, 0, 1, A, None) == 2         # no pages per workgroup
+    assert g(A, A + 8, A, 16, 4, 1, A, None) == 2     # pool not 16-byte aligned
 
 
 def test_kernel_and_split_choice_follow_the_cu_count(capi):

@@ -107,3 +107,34 @@ def test_read_bandwidth_probe_runs(fa, dev):
     fa.probe.probe_read_bw(x, sink, 64)
     torch.cuda.synchronize()
     assert sink.item() == 0x9e3779b9 - (1 << 32)
+
+
+@pytest.mark.parametrize("nontemporal", [True, False])
+def test_gather_bandwidth_probe_reads_every_page(fa, dev, nontemporal):
+    """The gather probe reads each page of both pools once through the table
+    (all-zero pools leave the sink alone; one trigger vector in the V page a
+    table entry names sets it), and clamps out-of-range ids into the pool."""
+    pages = 300
+    k = torch.zeros(pages * 1024, dtype=torch.int32, device=dev)
+    v = torch.zeros(pages * 1024, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(3)
+    table = torch.randperm(pages, generator=g).to(torch.int32).to(dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for per in (1, 7, 65, 300):
+        fa.probe.probe_gather_bw(k, v, table, sink, per, nontemporal)
+    torch.cuda.synchronize()
+    assert sink.item() == 0
+    target = int(table[-1].item())                  # the page of the last table entry
+    v.view(pages, 256, 4)[target, 200, 0] = 0x9e3779b9 - (1 << 32)
+    fa.probe.probe_gather_bw(k, v, table, sink, 65, nontemporal)
+    torch.cuda.synchronize()
+    assert sink.item() == 0x9e3779b9 - (1 << 32)
+    # out-of-range ids read page 0 or the last page instead
+    sink.zero_()
+    v.zero_()
+    bad = torch.zeros(pages, dtype=torch.int32, device=dev)   # every entry page 0 ...
+    bad[5], bad[6] = pages + 1000, -7                          # ... but these two
+    v.view(pages, 256, 4)[pages - 1, 3, 0] = 0x9e3779b9 - (1 << 32)
+    fa.probe.probe_gather_bw(k, v, bad, sink, 65, nontemporal)
+    torch.cuda.synchronize()
+    assert sink.item() == 0x9e3779b9 - (1 << 32)
