@@ -208,15 +208,19 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
     kb, vb, qb = kp.bfloat16(), vp.bfloat16(), q.bfloat16()
     ms_bf16 = median_of(lambda: fa.decode_paged(qb, kb, vb, tt, tc, S), reps, 3, iters, torch)
     del kb, vb, kp, vp
-    # GQA: the same contexts with 8 KV heads shared by groups of 4 query heads.
-    # Bytes count each KV page once (what a group-aware kernel must read).
-    Hkv = 8
-    kp = torch.randn(P, Hkv, 16, D, device=dev, dtype=torch.float16, generator=g)
-    vp = torch.randn(P, Hkv, 16, D, device=dev, dtype=torch.float16, generator=g)
-    ms_gqa = median_of(lambda: fa.decode_paged(q, kp, vp, tt, tc, S), reps, 3, iters, torch)
-    alg_gqa = kv_bytes * Hkv / H + other
-    del kp, vp
-    torch.cuda.empty_cache()
+    # GQA: the same contexts with 8 KV heads shared by groups of 4 query heads,
+    # and with 4 KV heads (groups of 8). Bytes count each KV page once (what a
+    # group-aware kernel must read).
+    gqa = {}
+    for Hkv in (8, 4):
+        kp = torch.randn(P, Hkv, 16, D, device=dev, dtype=torch.float16, generator=g)
+        vp = torch.randn(P, Hkv, 16, D, device=dev, dtype=torch.float16, generator=g)
+        ms_g = median_of(lambda: fa.decode_paged(q, kp, vp, tt, tc, S), reps, 3, iters, torch)
+        alg_g = kv_bytes * Hkv / H + other
+        gqa[Hkv] = {"ms": round(ms_g, 5), "algorithmic_bytes": alg_g,
+                    "GBps_unique_kv": round(alg_g / (ms_g * 1e-3) / 1e9, 1)}
+        del kp, vp
+        torch.cuda.empty_cache()
     return {
         "workload": "decode B32 H32 D128 ctx~U[512,32768] seed5, 16-token pages, 16 splits",
         "ms": round(ms, 5), "ms_split_pass": round(ms_split, 5),
@@ -224,8 +228,8 @@ def bench_decode(fa, torch, dev, reps=5, iters=20):
         "GBps": round(alg / (ms * 1e-3) / 1e9, 1),
         "pct_hbm_peak": round(100 * alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
         "split_pass_GBps": round(alg / (ms_split * 1e-3) / 1e9, 1),
-        "gqa_H32_Hkv8": {"ms": round(ms_gqa, 5), "algorithmic_bytes": alg_gqa,
-                         "GBps_unique_kv": round(alg_gqa / (ms_gqa * 1e-3) / 1e9, 1)},
+        "gqa_H32_Hkv8": gqa[8],
+        "gqa_H32_Hkv4": gqa[4],
         "bf16": {"ms": round(ms_bf16, 5), "GBps": round(alg / (ms_bf16 * 1e-3) / 1e9, 1),
                  "pct_hbm_peak": round(100 * alg / (ms_bf16 * 1e-3) / 1e9 / PEAK_HBM_GBS, 2)},
     }

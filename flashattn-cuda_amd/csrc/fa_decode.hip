@@ -7,15 +7,15 @@
 //
 // Pool layout: [num_pages, H_kv, 16, D] fp16 or bf16 (H_kv = H, or fewer KV heads
 // shared by groups of H / H_kv query heads), so the 16 tokens of one head in a
-// page are 16*D*2 contiguous bytes (4 KiB at D=128): one wave reads a page of
-// one head as fully coalesced 16-byte loads.
+// page are 16*D*2 contiguous bytes (4 KiB at D=128), copied into LDS as
+// contiguous 1 KiB requests.
 //
-// Split kernel: one workgroup (4 waves) per (split, head, sequence). Wave w
-// walks pages p0+w, p0+w+4, ...; lane l covers the 16-byte chunk l % (D/8)
-// of tokens l / (D/8) + (512/D) i of the page (i < D/32), so every load
-// instruction reads 1 KiB of the page contiguously. Each wave keeps its own
-// running max/sum and fp32 partial output; the four waves merge through LDS
-// at the end.
+// Split kernel: one workgroup (4 waves) per (split, KV head, up to 16 query
+// heads of its group, sequence); wave w walks pages p0+w, p0+w+4, ... and
+// computes the scores of every head of the workgroup and their PV products
+// on the matrix cores, so a page is read once per KV head. Each wave keeps
+// its own running max/sum and fp32 partial output per head; the four waves
+// merge through LDS at the end.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -32,26 +32,19 @@ constexpr int kPage = 16;
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / 64;
 
-// Element types of q, the pools and O: fp16, or bf16 (BF16 = true). Products
-// of two 16-bit values are exact in fp32; the dot product accumulates in fp32
-// (v_dot2_f32_f16 / v_dot2_f32_bf16) and everything after it is fp32.
+// Element types of q, the pools and O: fp16, or bf16 (BF16 = true). The
+// matrix products take them as 16-bit operands with fp32 accumulation; P is
+// rounded to the same 16-bit type for its product with V, everything else
+// is fp32.
 template <bool BF16>
 struct DecT {
   using e = f16;
   using v8 = f16x8;
-  using v2 = f16x2;
-  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
-    return __builtin_amdgcn_fdot2(a, b, c, false);
-  }
 };
 template <>
 struct DecT<true> {
   using e = __bf16;
   using v8 = bf16x8;
-  using v2 = bf16x2;
-  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
-  }
 };
 
 // Longest sequence first: grid index z (the slowest-varying one, so low z
@@ -80,6 +73,77 @@ __device__ __forceinline__ int sequence_of_rank(const int32_t* __restrict__ ctx_
   return *sh_seq;
 }
 
+// Split kernel, on the matrix cores: one workgroup (4 waves) per (split, KV
+// head, up to 16 of the query heads that share it, sequence). A wave copies each
+// page's K and V rows of the KV head into LDS (1 KiB per copy instruction,
+// contiguous in the pool, non-temporal), then
+//   S   = K Q^T   (v_mfma_f32_16x16x32: 16 tokens x 16 heads, K from LDS,
+//                  Q^T in registers; heads past the group are zero columns)
+//   P   = exp2(S c - m) per head column (online softmax, in registers)
+//   O^T += V^T P^T (v_mfma_f32_16x16x16 per 16 columns of D: V^T read with
+//                  ds_read_b64_tr_b16, P^T straight from the S accumulator)
+// so each page is read once for every query head of its group. Lane l holds
+// head l % 16 and tokens 4 (l / 16) .. + 3 of S, and rows 4 (l / 16) + r of
+// every 16-column block of O^T for the same head, so the softmax statistics
+// of a head stay in its lane column. Each wave keeps two page slots (the
+// next page's copies land while the current one is computed).
+//
+// LDS layout of a page slot: row t (token) of 16-byte chunks, chunk c stored
+// at position c ^ (t % (D / 8)), the forward's K-tile swizzle. The copies
+// apply it on the source side: lane l of copy i fills LDS chunk 64 i + l from
+// the page chunk it should hold. (SQ_LDS_BANK_CONFLICT still counts ~30 % of
+// the LDS-active cycles, all in the K reads; the kernel waits on memory for
+// ~74 % of its wave cycles, and a conflict-free variant of the swizzle for a
+// 64-bank model timed the same.)
+template <int D>
+__device__ __forceinline__ int dec_swz(int t) { return t & (D / 8 - 1); }
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mma16k32(f16x8 a, f16x8 b, f32x4 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mma16k16(f16x4 a, f16x4 b, f32x4 c) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+}
+
+// 16-byte copy straight into LDS with the non-temporal hint (the page is read
+// once): see dma16.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(r)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ float max_cols(float x) {   // max over the 4 lane groups of a column
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float sum_cols(float x) {   // sum over the 4 lane groups of a column
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int D, bool BF16>
 __global__ void __launch_bounds__(kDecThreads)
 fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
@@ -87,26 +151,32 @@ fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
                        const typename DecT<BF16>::e* __restrict__ vpool,
                        const int32_t* __restrict__ page_table,
                        const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
-                       float* __restrict__ part_lse, int H, int Hkv, int max_pages, int num_pages,
-                       int S, float c) {
+                       float* __restrict__ part_lse, int H, int Hkv, int max_pages,
+                       int num_pages, int S, float c) {
   using T = DecT<BF16>;
-  using v8 = typename T::v8;
-  using v2 = typename T::v2;
-  constexpr int CH = D / 8;          // 16-byte chunks of a token row
-  constexpr int TPI = 64 / CH;       // tokens per load instruction (1 KiB contiguous)
-  constexpr int NI = kPage / TPI;    // load instructions per page and pool
-  __shared__ float sh_o[kDecWaves][D];
-  __shared__ float sh_m[kDecWaves];
-  __shared__ float sh_l[kDecWaves];
+  constexpr int PAGE = kPage * D * 2;   // bytes of one head's page
+  constexpr int CPR = D / 8;            // 16-byte chunks per token row
+  constexpr int KB = D / 32;            // k-steps of S = K Q^T
+  constexpr int DB = D / 16;            // 16-column blocks of O^T
+  constexpr int NC = PAGE / 1024;       // 1 KiB copies per page and pool
+  static_assert(kDecWaves * 16 * D * 4 <= kDecWaves * 4 * PAGE, "merge area within the slots");
+  __shared__ __attribute__((aligned(1024))) char smem[kDecWaves * 4 * PAGE];
+  __shared__ float sh_m[kDecWaves][16];
+  __shared__ float sh_l[kDecWaves][16];
   __shared__ int sh_bad;
   __shared__ int sh_ctx[kDecThreads];
   __shared__ int sh_seq;
 
-  const int s = blockIdx.x, h = blockIdx.y;
+  const int s = blockIdx.x;
+  const int group = H / Hkv;
+  const int ngrp = (group + 15) / 16;
+  const int hk = blockIdx.y / ngrp;
+  const int h0 = hk * group + 16 * (blockIdx.y % ngrp);   // first query head of this workgroup
+  const int G = min(16, hk * group + group - h0);
   const int b = sequence_of_rank(ctx_lens, (int)gridDim.z, (int)blockIdx.z, sh_ctx, &sh_seq);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ch = lane % CH;    // chunk: d = 8 ch .. 8 ch + 7
-  const int tl = lane / CH;    // token tl + TPI i of load instruction i
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
 
   if (tid == 0) sh_bad = 0;
   __syncthreads();
@@ -120,298 +190,146 @@ fa_decode_split_kernel(const typename DecT<BF16>::e* __restrict__ q,
   const int p0 = min(s * chunk, pages);
   const int p1 = min(p0 + chunk, pages);
 
-  v2 qv[4];
-  {
-    const v8 x = *reinterpret_cast<const v8*>(q + ((size_t)b * H + h) * D + 8 * ch);
+  // Q^T operand (16x16x32 B): column col = head h0 + col, rows 8 grp .. + 7
+  // of k-step kb.
+  f16x8 qf[KB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) qv[e] = v2{x[2 * e], x[2 * e + 1]};
+  for (int kb = 0; kb < KB; ++kb) {
+    qf[kb] = f16x8{};
+    if (col < G)
+      qf[kb] = __builtin_bit_cast(f16x8, *reinterpret_cast<const typename T::v8*>(
+                                             q + ((size_t)b * H + h0 + col) * D + 32 * kb + 8 * grp));
   }
 
   float m = -INFINITY, l = 0.f;
-  float o[8];
+  f32x4 o[DB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+  for (int db = 0; db < DB; ++db) o[db] = f32x4{};
 
+  // Copy offsets: lane l of copy i fills LDS chunk L = 64 i + l with page
+  // chunk (L % CPR) ^ swz(row) of row L / CPR.
+  uint32_t coff[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int L = 64 * i + lane, t = L / CPR;
+    coff[i] = (uint32_t)((t * CPR + ((L % CPR) ^ dec_swz<D>(t))) * 16);
+  }
+  const uint32_t lds0 = lds_addr(smem) + (uint32_t)(wave * 4 * PAGE);   // this wave's two slots
   const int32_t* pt = page_table + (size_t)b * max_pages;
-  const int kvh = h / (H / Hkv);
-  // The wave's next page is loaded into (kn, vn) before the current one is
-  // used, so one page per wave is always in flight behind the arithmetic.
-  // Load instruction i of a pool reads bytes 1024 i .. 1024 i + 1023 of the
-  // page (lane l: 16 bytes at 16 l), with the non-temporal hint: each page
-  // is read once, and whole contiguous 1 KiB requests let the hint stream it
-  // (a layout in which each instruction touched every line of the page ran
-  // 57 % slower with the hint and no faster without it).
-  v8 kn[NI], vn[NI];
-  bool ok_n = false;
-  auto load_page = [&](int p) {
-    const int pid = pt[p];
-    ok_n = pid >= 0 && pid < num_pages;
-    if (!ok_n) return;
-    const size_t base = ((size_t)pid * Hkv + kvh) * (kPage * D) + 8 * (size_t)lane;
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      kn[i] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(kpool + base + 512 * i));
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      vn[i] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(vpool + base + 512 * i));
+  // Page ids of the wave's pages p0 + wave + 4 k, 64 at a time: lane i of
+  // pidv holds the id of page k = 64 j + i, read with readlane (a page
+  // table load per page would wait for every copy in flight before it).
+  int pidv = -1;
+  auto page_id = [&](int k) -> int {
+    if ((k & 63) == 0) {
+      const int pi = p0 + wave + 4 * (k + lane);
+      pidv = pi < p1 ? pt[pi] : -1;
+    }
+    return __builtin_amdgcn_readlane(pidv, k & 63);
   };
-  if (p0 + wave < p1) load_page(p0 + wave);
-  for (int p = p0 + wave; p < p1; p += kDecWaves) {
-    v8 kv[NI], vv[NI];
+  // Issue the copies of the wave's k-th page into slot sl; false (nothing
+  // issued) for an invalid page id.
+  auto issue = [&](int k, int sl) -> bool {
+    const int pid = page_id(k);
+    if (pid < 0 || pid >= num_pages) return false;
+    const size_t off = ((size_t)pid * Hkv + hk) * (size_t)(kPage * D);
+    const auto rk = make_rsrc_s(kpool + off, PAGE);
+    const auto rv = make_rsrc_s(vpool + off, PAGE);
+    const uint32_t dk = lds0 + (uint32_t)(sl * 2 * PAGE);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      kv[i] = kn[i];
-      vv[i] = vn[i];
+    for (int i = 0; i < NC; ++i) dma16_nt(rk, dk + 1024 * i, coff[i]);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) dma16_nt(rv, dk + PAGE + 1024 * i, coff[i]);
+    return true;
+  };
+
+  // Per-lane LDS offsets of the operand reads within a slot.
+  // K (16x16x32 A): row col, chunk 4 kb + grp.
+  // V^T (16x16x16 A through ds_read_b64_tr_b16): lane (grp, s) supplies row
+  // 4 grp + s / 4, 8 bytes at column 16 db + 4 (s % 4).
+  const int vrow = 4 * grp + (col >> 2);
+  int p = p0 + wave;
+  int sl = 0, k = 0;
+  bool ok = p < p1 && issue(0, 0);
+  for (; p < p1; p += kDecWaves, sl ^= 1, ++k) {
+    const int pn = p + kDecWaves;
+    const bool ok_n = pn < p1 && issue(k + 1, sl ^ 1);
+    if (ok_n) wait_vmcnt<2 * NC>(); else wait_vmem();
+    if (!ok) { bad = true; ok = ok_n; continue; }
+    const uint32_t ks = lds0 + (uint32_t)(sl * 2 * PAGE);
+    const uint32_t vs = ks + PAGE;
+    f32x4 sc = f32x4{};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const lds_cp a = (lds_cp)(size_t)(ks + (uint32_t)((col * CPR + ((4 * kb + grp) ^ dec_swz<D>(col))) * 16));
+      sc = mma16k32<BF16>(lds_b128(a), qf[kb], sc);
     }
-    const bool ok = ok_n;
-    if (p + kDecWaves < p1) load_page(p + kDecWaves);
-    if (!ok) { bad = true; continue; }
-    float st[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      float d = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) d = T::dot2(qv[e], v2{kv[i][2 * e], kv[i][2 * e + 1]}, d);
-      st[i] = d;
-    }
-#pragma unroll
-    for (int sh = 1; sh < CH; sh <<= 1)
-#pragma unroll
-      for (int i = 0; i < NI; ++i) st[i] += __shfl_xor(st[i], sh, 64);
+    // Scores of head col, tokens 4 grp + r of the page; slots past the
+    // context get -inf (their K rows may hold anything, NaN included).
+    const int tok0 = p * kPage + 4 * grp;
+    float st[4];
     float mp = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      st[i] *= c;
-      if (p * kPage + TPI * i + tl >= ctx) {
-        // A slot past the context holds whatever the pool held (NaN and
-        // Inf included): its score is -inf and its V row is dropped, since
-        // 0 * NaN would poison the output.
-        st[i] = -INFINITY;
-        vv[i] = v8{};
-      }
-      mp = fmaxf(mp, st[i]);
+    for (int r = 0; r < 4; ++r) {
+      st[r] = tok0 + r < ctx ? sc[r] * c : -INFINITY;
+      mp = fmaxf(mp, st[r]);
     }
-#pragma unroll
-    for (int sh = CH; sh < 64; sh <<= 1) mp = fmaxf(mp, __shfl_xor(mp, sh, 64));
+    mp = max_cols(mp);
     const float m_new = fmaxf(m, mp);   // finite: token p*16 < ctx
     const float alpha = (m_new == m) ? 1.f : exp2_hw(m - m_new);
-    float pr[NI];
+    float pr[4];
     float ps = 0.f;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      pr[i] = exp2_hw(st[i] - m_new);
-      ps += pr[i];
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = exp2_hw(st[r] - m_new);
+      ps += pr[r];
     }
     l = l * alpha + ps;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = o[e] * alpha;
-#pragma unroll
-      for (int i = 0; i < NI; ++i) a = fmaf(pr[i], (float)vv[i][e], a);
-      o[e] = a;
-    }
     m = m_new;
+    const f16x2 p01 = cvt2x<BF16>(pr[0], pr[1]);
+    const f16x2 p23 = cvt2x<BF16>(pr[2], pr[3]);
+    const f16x4 pb = f16x4{p01[0], p01[1], p23[0], p23[1]};
+    // bf16 keeps 8 significant bits of P: a second product with the rounded
+    // remainder p - bf16(p) carries P to 16 (fp16's 11 are kept as they are).
+    f16x4 pl = f16x4{};
+    if constexpr (BF16) {
+      auto up = [](f16 h) { return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, h) << 16); };
+      const f16x2 l01 = cvt2x<true>(pr[0] - up(pb[0]), pr[1] - up(pb[1]));
+      const f16x2 l23 = cvt2x<true>(pr[2] - up(pb[2]), pr[3] - up(pb[3]));
+      pl = f16x4{l01[0], l01[1], l23[0], l23[1]};
+    }
+    const bool tail = p * kPage + kPage > ctx;   // wave-uniform: the sequence's last, partial page
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int cb = 2 * db + ((col & 3) >> 1);   // chunk of columns 16 db + 4 (s % 4)
+      const lds_cp a = (lds_cp)(size_t)(vs + (uint32_t)((vrow * CPR + (cb ^ dec_swz<D>(vrow))) * 16 + 8 * (col & 1)));
+      f16x4 va = lds_tr16(a);
+      if (tail) {   // V rows past the context may hold NaN or Inf: 0 * NaN
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (tok0 + e >= ctx) va[e] = (f16)0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[db][e] *= alpha;
+      o[db] = mma16k16<BF16>(va, pb, o[db]);
+      if constexpr (BF16) o[db] = mma16k16<true>(va, pl, o[db]);
+    }
+    ok = ok_n;
   }
+  l = sum_cols(l);
 
-  // Sum the token groups that share a chunk of D.
-#pragma unroll
-  for (int sh = CH; sh < 64; sh <<= 1) {
-    l += __shfl_xor(l, sh, 64);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] += __shfl_xor(o[i], sh, 64);
-  }
+  // Merge the waves through LDS (the page slots are free once every wave's
+  // copies have landed and its reads are done).
+  wait_vmem();
   if (bad) sh_bad = 1;
-  if (tl == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sh_o[wave][8 * ch + i] = o[i];
-    if (ch == 0) { sh_m[wave] = m; sh_l[wave] = l; }
-  }
   __syncthreads();
-
-  const size_t pidx = ((size_t)b * H + h) * S + s;
-  if (tid < D) {
-    float M = sh_m[0];
+  float* sh_o = reinterpret_cast<float*>(smem);   // [kDecWaves][16][D]
+  if (col < G) {
 #pragma unroll
-    for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, sh_m[w]);
-    float acc = 0.f, z = 0.f;
-    if (M != -INFINITY) {
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) {
-        const float e = (sh_m[w] == -INFINITY) ? 0.f : exp2_hw(sh_m[w] - M);
-        acc += e * sh_o[w][tid];
-        z += e * sh_l[w];
-      }
-    }
-    float out = (z > 0.f) ? acc / z : 0.f;
-    float lse = (z > 0.f) ? (M + log2_hw(z)) * kLn2 : -INFINITY;
-    if (sh_bad) { out = NAN; lse = NAN; }
-    part_o[pidx * D + tid] = out;
-    if (tid == 0) part_lse[pidx] = lse;
-  }
-}
-
-// Grouped-KV split pass: one workgroup per (split, G query heads that share
-// one KV head, sequence). Each K/V page is loaded once into registers and
-// used for all G heads (a lane's dot products, softmax state and output
-// slice are kept per head), so a page is read once per KV head instead of
-// once per query head. Waves split the pages as above and merge per head.
-//
-// LPT lanes share a token: with LPT = 4 a lane holds D / 4 columns of one
-// token of the page; with LPT = 8 it holds D / 8 columns of two tokens
-// (t and t + 8), which halves the per-head query and output registers so
-// that four heads fit at D = 128.
-template <int D, int G, bool BF16, int LPT = 4>
-__global__ void __launch_bounds__(kDecThreads)
-fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
-                             const typename DecT<BF16>::e* __restrict__ kpool,
-                             const typename DecT<BF16>::e* __restrict__ vpool,
-                             const int32_t* __restrict__ page_table,
-                             const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
-                             float* __restrict__ part_lse, int H, int Hkv, int max_pages,
-                             int num_pages, int S, float c) {
-  using T = DecT<BF16>;
-  using v8 = typename T::v8;
-  using v2 = typename T::v2;
-  static_assert(LPT == 4 || LPT == 8, "4 or 8 lanes per token");
-  constexpr int DPL = D / LPT;   // d per lane
-  constexpr int NV = DPL / 8;    // 16-byte vectors per lane per row
-  constexpr int TPL = LPT / 4;   // tokens per lane: tok + 8 j
-  __shared__ float sh_o[kDecWaves][G][D];
-  __shared__ float sh_m[kDecWaves][G];
-  __shared__ float sh_l[kDecWaves][G];
-  __shared__ int sh_bad;
-  __shared__ int sh_ctx[kDecThreads];
-  __shared__ int sh_seq;
-
-  const int s = blockIdx.x, hg = blockIdx.y;
-  const int b = sequence_of_rank(ctx_lens, (int)gridDim.z, (int)blockIdx.z, sh_ctx, &sh_seq);
-  const int h0 = hg * G;                  // first query head of this workgroup
-  const int hk = h0 / (H / Hkv);          // their KV head (G divides H / Hkv)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tok = lane / LPT;
-  const int dq = lane % LPT;
-
-  if (tid == 0) sh_bad = 0;
-  __syncthreads();
-
-  int ctx = ctx_lens[b];
-  bool bad = false;
-  if (ctx < 0) { bad = true; ctx = 0; }
-  int pages = (ctx + kPage - 1) / kPage;
-  if (pages > max_pages) { bad = true; pages = max_pages; ctx = max_pages * kPage; }
-  const int chunk = (pages + S - 1) / S;
-  const int p0 = min(s * chunk, pages);
-  const int p1 = min(p0 + chunk, pages);
-
-  v2 qv[G][DPL / 2];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const typename T::e* qp = q + ((size_t)b * H + h0 + g) * D + dq * DPL;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      v8 x = *reinterpret_cast<const v8*>(qp + 8 * i);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) qv[g][4 * i + e] = v2{x[2 * e], x[2 * e + 1]};
-    }
-  }
-
-  float m[G], l[G];
-  float o[G][DPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) o[g][i] = 0.f;
-  }
-
-  const int32_t* pt = page_table + (size_t)b * max_pages;
-  for (int p = p0 + wave; p < p1; p += kDecWaves) {
-    const int pid = pt[p];
-    if (pid < 0 || pid >= num_pages) { bad = true; continue; }
-    const size_t base = ((size_t)pid * Hkv + hk) * (kPage * D) + (size_t)tok * D + dq * DPL;
-    v8 kv[TPL][NV], vv[TPL][NV];
-#pragma unroll
-    for (int j = 0; j < TPL; ++j) {
-#pragma unroll
-      for (int i = 0; i < NV; ++i) kv[j][i] = *reinterpret_cast<const v8*>(kpool + base + j * 8 * D + 8 * i);
-    }
-#pragma unroll
-    for (int j = 0; j < TPL; ++j) {
-#pragma unroll
-      for (int i = 0; i < NV; ++i) vv[j][i] = *reinterpret_cast<const v8*>(vpool + base + j * 8 * D + 8 * i);
-    }
-    bool live[TPL];
-#pragma unroll
-    for (int j = 0; j < TPL; ++j) {
-      live[j] = p * kPage + tok + 8 * j < ctx;
-      if (!live[j]) {   // slot past the context: drop its V row (it may hold NaN or Inf)
-#pragma unroll
-        for (int i = 0; i < NV; ++i) vv[j][i] = v8{};
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float st[TPL];
-      float mp = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < TPL; ++j) {
-        float dot = 0.f;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            dot = T::dot2(qv[g][4 * i + e], v2{kv[j][i][2 * e], kv[j][i][2 * e + 1]}, dot);
-          }
-        }
-#pragma unroll
-        for (int sh = 1; sh < LPT; sh <<= 1) dot += __shfl_xor(dot, sh, 64);
-        st[j] = live[j] ? dot * c : -INFINITY;
-        mp = fmaxf(mp, st[j]);
-      }
-#pragma unroll
-      for (int sh = LPT; sh < 64; sh <<= 1) mp = fmaxf(mp, __shfl_xor(mp, sh, 64));
-      const float m_new = fmaxf(m[g], mp);   // finite: token p*16 < ctx
-      const float alpha = (m_new == m[g]) ? 1.f : exp2_hw(m[g] - m_new);
-      float pr[TPL];
-      float psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < TPL; ++j) {
-        pr[j] = exp2_hw(st[j] - m_new);
-        psum += pr[j];
-      }
-      l[g] = l[g] * alpha + psum;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float acc = o[g][8 * i + e] * alpha;
-#pragma unroll
-          for (int j = 0; j < TPL; ++j) acc = fmaf(pr[j], (float)vv[j][i][e], acc);
-          o[g][8 * i + e] = acc;
-        }
-      }
-      m[g] = m_new;
-    }
-  }
-
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int sh = LPT; sh < 64; sh <<= 1) {
-      l[g] += __shfl_xor(l[g], sh, 64);
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) o[g][i] += __shfl_xor(o[g][i], sh, 64);
-    }
-  }
-  if (bad) sh_bad = 1;
-  if (tok == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) sh_o[wave][g][dq * DPL + i] = o[g][i];
-      if (dq == 0) { sh_m[wave][g] = m[g]; sh_l[wave][g] = l[g]; }
-    }
+      for (int r = 0; r < 4; ++r) sh_o[(wave * 16 + col) * D + 16 * db + 4 * grp + r] = o[db][r];
+    if (grp == 0) { sh_m[wave][col] = m; sh_l[wave][col] = l; }
   }
   __syncthreads();
 
@@ -426,7 +344,7 @@ fa_decode_split_group_kernel(const typename DecT<BF16>::e* __restrict__ q,
 #pragma unroll
       for (int w = 0; w < kDecWaves; ++w) {
         const float e = (sh_m[w][g] == -INFINITY) ? 0.f : exp2_hw(sh_m[w][g] - M);
-        acc += e * sh_o[w][g][d];
+        acc += e * sh_o[(w * 16 + g) * D + d];
         z += e * sh_l[w][g];
       }
     }
@@ -494,29 +412,9 @@ static int decode_split(const void* q, const void* k_pool, const void* v_pool,
   const E* Q = (const E*)q;
   const E* Kp = (const E*)k_pool;
   const E* Vp = (const E*)v_pool;
-  // Grouped KV heads: G query heads per workgroup share each page read. At
-  // D = 128 four heads take 8 lanes per token (two tokens per lane), which
-  // keeps their state within the registers of three waves per SIMD; with 4
-  // lanes per token they needed 256 VGPRs (one wave per SIMD: 706 us vs 507 us
-  // for G = 2 on the group-of-4 pools).
+  // One workgroup per (split, KV head, 16 of its query heads, sequence).
   const int64_t group = H / Hkv;
-  const int G = group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
-  if (G > 1) {
-    const dim3 ggrid((unsigned)num_splits, (unsigned)(H / G), (unsigned)B);
-#define FA_DEC_GROUP(DD, GG, LL)                                                                    \
-  hipLaunchKernelGGL((fa_decode_split_group_kernel<DD, GG, BF16, LL>), ggrid, dim3(kDecThreads), 0, \
-                     s, Q, Kp, Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,         \
-                     (int)max_pages, (int)num_pages, (int)num_splits, c)
-    if (D == 128) {
-      if (G == 4) FA_DEC_GROUP(128, 4, 8); else FA_DEC_GROUP(128, 2, 4);
-    } else {
-      if (G == 4) FA_DEC_GROUP(64, 4, 4); else FA_DEC_GROUP(64, 2, 4);
-    }
-#undef FA_DEC_GROUP
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? FA_OK : -(int)e;
-  }
-  dim3 grid((unsigned)num_splits, (unsigned)H, (unsigned)B);
+  const dim3 grid((unsigned)num_splits, (unsigned)(Hkv * ((group + 15) / 16)), (unsigned)B);
   if (D == 128) {
     hipLaunchKernelGGL((fa_decode_split_kernel<128, BF16>), grid, dim3(kDecThreads), 0, s, Q, Kp,
                        Vp, page_table, ctx_lens, part_o, part_lse, (int)H, (int)Hkv,

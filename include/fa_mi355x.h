@@ -248,7 +248,9 @@ int64_t fa_decode_workspace_floats(int64_t B, int64_t H, int64_t D,
 
 /*
  * Split pass of the paged decode: for each (sequence b, head h, split s) the
- * normalised partial attention of q[b,h] over the split's pages.
+ * normalised partial attention of q[b,h] over the split's pages (QK and PV
+ * on fp16 matrix-core products with fp32 accumulation; P rounded to fp16
+ * for the PV product).
  * Sequence b has ceil(ctx_lens[b]/page_size) pages, divided into num_splits
  * runs of ceil(pages/num_splits) pages. An empty split writes part_o = 0 and
  * part_lse = -inf. A page id outside [0, num_pages) makes the partials of
@@ -320,8 +322,9 @@ int fa_decode_paged_noalloc_f16(const void* q, const void* k_pool, const void* v
 
 /*
  * fa_decode_paged_gqa_f16 for bf16 q, pools and O (same layouts and
- * arguments; QK dot products in fp32 from bf16 pairs, softmax and merges in
- * fp32, O rounded to bf16 to nearest even). No reference counterpart (the
+ * arguments; QK products of bf16 pairs accumulated in fp32, P carried into
+ * the PV product as two bf16 terms (~16 significant bits), softmax and merges
+ * in fp32, O rounded to bf16 to nearest even). No reference counterpart (the
  * reference has neither a decode path nor bf16).
  */
 int fa_decode_paged_bf16(const void* q, const void* k_pool, const void* v_pool,

@@ -160,9 +160,10 @@ def _pages(rng, B, ctx, Hkv, D, extra=2):
 @pytest.mark.parametrize("S", [1, 3, 16])
 def test_bf16_decode_vs_oracle(fa, dev, D, Hkv, S):
     """decode_paged with bf16 q and pools. The QK products of bf16 pairs are
-    exact in fp32 and P and V stay fp32, so only O's final rounding to bf16
-    separates it from the fp32 oracle on the bf16-rounded inputs:
-    |O - O_ref| <= 1e-3 + half a bf16 ulp of O_ref; L relative <= 1e-4."""
+    exact in fp32, and P enters the PV product as the sum of two bf16 values
+    (about 16 significant bits) against exact bf16 V, so O's final rounding to
+    bf16 dominates its distance from the fp32 oracle on the bf16-rounded
+    inputs: |O - O_ref| <= 1e-3 + half a bf16 ulp of O_ref; L relative <= 1e-4."""
     B, H = 5, 4
     ctx = [1, 15, 16, 17, 300]
     rng = np.random.default_rng(D + 10 * Hkv + S)
