@@ -164,10 +164,12 @@ def test_gqa_rejects_bad_head_counts(fa, dev):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("H,Hkv", [(8, 4), (8, 2), (12, 2), (6, 2)])
-def test_gqa_decode_group_kernel(fa, dev, D, H, Hkv):
-    """Groups of 2 and 4 query heads per workgroup (and group 3, which uses one
-    head per workgroup) against the decode oracle over repeated pools,
+@pytest.mark.parametrize("H,Hkv", [(8, 4), (8, 2), (12, 2), (6, 2), (16, 2), (32, 2), (40, 2),
+                                   (32, 1)])
+def test_gqa_decode_groups(fa, dev, D, H, Hkv):
+    """Groups of 2 to 32 query heads per KV head (a workgroup takes up to 16
+    of them: groups of 20 and 32 span two workgroups, groups of 3 and 6 leave
+    columns of the 16 unused) against the decode oracle over repeated pools,
     including an invalid page id (NaN for that sequence only)."""
     B = 3
     rng = np.random.default_rng(H * 10 + Hkv + D)
