@@ -160,3 +160,32 @@ def test_rejects_bad_arguments(fa, dev):
         fa.kv_append(kn, kn, p8, p8.clone(), tab, st)
     with pytest.raises(RuntimeError, match="int32"):
         fa.kv_append(kn, kn, kp, kp.clone(), tab.long(), st)
+
+
+@pytest.mark.parametrize("D,Hkv", [(64, 8), (128, 2)])
+def test_decode_agrees_with_causal_forward(fa, dev, D, Hkv):
+    """The serving invariant between the two paths: K and V written into pages
+    by kv_append, then decoding the query of position t over the first t + 1
+    tokens gives row t of the causal forward over the same Q, K, V (both
+    against the same fp32 oracle at the forward's bars: O within 2e-3 each, so
+    4e-3 apart at most; L within 1e-4 relative)."""
+    B, H, N = 2, 8, 1000
+    g = torch.Generator(device=dev).manual_seed(D + Hkv)
+    q = torch.randn(B, H, N, D, device=dev, generator=g).half()
+    k = torch.randn(B, Hkv, N, D, device=dev, generator=g).half()
+    v = torch.randn(B, Hkv, N, D, device=dev, generator=g).half()
+    O, L = fa.forward(q, k, v, causal=True)
+    pages = (N + 15) // 16
+    table = torch.randperm(B * pages, device=dev, generator=g).to(torch.int32).view(B, pages)
+    kp = torch.zeros(B * pages, Hkv, 16, D, dtype=torch.half, device=dev)
+    vp = torch.zeros_like(kp)
+    bad = fa.kv_append(k, v, kp, vp, table, torch.zeros(B, dtype=torch.int32, device=dev))
+    assert int(bad.sum()) == 0
+    for t in (0, 15, 16, 517, N - 1):
+        ctx = torch.full((B,), t + 1, dtype=torch.int32, device=dev)
+        Od, Ld = fa.decode_paged(q[:, :, t].contiguous(), kp, vp, table, ctx, 16)
+        torch.cuda.synchronize()
+        d_o = (Od.float() - O[:, :, t].float()).abs().max().item()
+        d_l = ((Ld - L[:, :, t]).abs() / L[:, :, t].abs().clamp(min=1)).max().item()
+        assert d_o <= 4e-3, f"t {t}: O differs by {d_o:.2e}"
+        assert d_l <= 1e-4, f"t {t}: L differs by {d_l:.2e}"
