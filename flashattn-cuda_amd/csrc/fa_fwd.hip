@@ -937,23 +937,32 @@ namespace fa {
 // Key splits for the torch forward on a device of `cus` compute units.
 static int splitkv_plan(int64_t B, int64_t H, int64_t N, int64_t D, int causal, int cus) {
   if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128) || cus <= 0) return 1;
-  // Measured: a split pays where the row blocks leave CUs idle and each split
-  // still has >= 32 key tiles (B1 H1 N16384: 122 -> 88 us with 2 splits);
-  // with fewer tiles per workgroup its fixed costs and the combine pass
-  // dominate (B1 H8 N1024: 11.5 -> 12.8 us + 7 us), and causal triangles did
-  // not even out (B1 H8 N4096 causal: 36.5 -> 42.6 us).
-  if (causal) return 1;
   // D = 64: the 64-row kernel (chosen where 128-row blocks leave CUs idle)
   // beat every split count (us: B1 H1 N16384 79.7 vs 85.6 with 2 splits, B1 H2
   // N8192 42.0 vs 49.5, B1 H1 N8192 31.6 vs 32.0 with 4, B1 H2 N4096 18.8 vs
-  // 23.1 with 4).
+  // 23.1 with 4; causal B1 H2 N8192 36.0 vs 44.0, B1 H4 N4096 19.8 vs 28.9).
   if (D == 64) return 1;
   const int64_t units = B * H * ((N + kBR - 1) / kBR);
   const int64_t tiles = (N + kBC - 1) / kBC;   // key tiles of a row block
-  if (units >= cus) return 1;
-  int64_t sp = (cus + units - 1) / units;
-  sp = sp < tiles / 32 ? sp : tiles / 32;
+  // D = 128 splits only where the splits of every row block still fit one
+  // wave of workgroups (B1 H3 N8192, 192 row blocks: 100.6 us unsplit,
+  // 125.2 with 2 splits; causal 84.6 vs 95.6).
+  if (2 * units > cus) return 1;
+  int64_t sp = cus / units;
   sp = sp < 8 ? sp : 8;
+  if (!causal) {
+    // At least 32 key tiles per split (B1 H1 N16384: 156.5 -> 137.8 us with
+    // 2 splits; B1 H8 N2048, 32 tiles: 27.3 vs 36.4 with 2).
+    sp = sp < tiles / 32 ? sp : tiles / 32;
+  } else {
+    // Causal row blocks differ in length, and the longest sets the time: a
+    // split evens them out down to 8 tiles per split (B1 H1 N8192 78.1 ->
+    // 43.4 us with 4 splits, B1 H1 N2048 25.2 -> 17.6 with 4, B1 H2 N8192
+    // 79.4 -> 68.0 with 2), but a 2-way split needs 64 tiles (B1 H4 N4096
+    // 43.6 -> 41.7; B1 H8 N2048, 32 tiles: 25.9 -> 34.5).
+    sp = sp < tiles / 8 ? sp : tiles / 8;
+    if (sp == 2 && tiles < 64) sp = 1;
+  }
   return sp < 2 ? 1 : (int)sp;
 }
 }  // namespace fa

@@ -360,4 +360,11 @@ def test_kernel_and_split_choice_follow_the_cu_count(capi):
     assert plan(1, 8, 4096, 128, 0, 256) == 1      # 256 blocks fill 256 CUs
     assert plan(1, 8, 4096, 128, 0, 512) == 2      # but not a 512-CU device
     assert plan(1, 1, 16384, 64, 0, 256) == 1      # D = 64 never splits
-    assert plan(1, 1, 16384, 128, 1, 256) == 1     # causal never splits
+    assert plan(1, 3, 8192, 128, 0, 256) == 1      # 192 blocks: two splits would not fit one wave
+    # causal D = 128: the longest row block sets the time; splits down to 8 tiles
+    assert plan(1, 1, 8192, 128, 1, 256) == 4      # 64 blocks, 128 tiles
+    assert plan(1, 1, 2048, 128, 1, 256) == 4      # 16 blocks, 32 tiles: 8 per split
+    assert plan(1, 4, 4096, 128, 1, 256) == 2      # 128 blocks, 64 tiles
+    assert plan(1, 8, 2048, 128, 1, 256) == 1      # 128 blocks, 32 tiles: 2 splits lose
+    assert plan(1, 3, 8192, 128, 1, 256) == 1      # 192 blocks
+    assert plan(1, 1, 16384, 64, 1, 256) == 1      # D = 64 never splits

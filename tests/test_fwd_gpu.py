@@ -412,17 +412,26 @@ def test_splitkv_plan_and_default_path(fa, dev):
     different summation order)."""
     p = fa.probe.probe_fwd_splitkv_plan
     assert p(1, 8, 4096, 64, 0) == 1          # the headline keeps the unsplit kernel
-    assert p(1, 8, 4096, 64, 1) == 1          # causal never splits
+    assert p(1, 8, 4096, 64, 1) == 1          # D = 64 never splits
+    assert p(1, 1, 8192, 128, 1) == 4         # causal D = 128 over few row blocks
     assert p(1, 8, 1024, 64, 0) == 1          # too few key tiles per split
     assert p(1, 1, 16384, 64, 0) == 1         # D = 64: the 64-row kernel instead
     assert p(1, 1, 16384, 128, 0) == 2
     assert p(1, 1, 8192, 128, 0) == 4
     Q, K, V = make_fwd_inputs(1, 1, 8192, 128, seed=77, amp=1.0)
     tq, tk, tv = _to_dev(dev, Q, K, V)
-    Od, Ld = fa.forward(tq, tk, tv)
-    Ou, Lu = fa.probe.probe_fwd_splitkv(tq, tk, tv, False, 1, True)
-    assert (Od.float() - Ou.float()).abs().max().item() <= 2e-3
-    assert ((Ld - Lu).abs() / Lu.abs().clamp(min=1)).max().item() <= 1e-5
+    for causal in (False, True):
+        Od, Ld = fa.forward(tq, tk, tv, causal=causal)
+        Ou, Lu = fa.probe.probe_fwd_splitkv(tq, tk, tv, causal, 1, True)
+        assert (Od.float() - Ou.float()).abs().max().item() <= 2e-3
+        assert ((Ld - Lu).abs() / Lu.abs().clamp(min=1)).max().item() <= 1e-5
+    # a causal shape the plan splits 4 ways, against the oracle
+    assert p(1, 1, 2048, 128, 1) == 4
+    Q, K, V = make_fwd_inputs(1, 1, 2048, 128, seed=78, amp=1.0)
+    tq, tk, tv = _to_dev(dev, Q, K, V)
+    O, L = fa.forward(tq, tk, tv, causal=True)
+    Or, Lr = naive_attention(half_cast(Q), half_cast(K), half_cast(V), causal=True)
+    _check(O, L, Or, Lr, 1.0, tag="default path, causal split 4 B1 H1 N2048 D128")
 
 
 def test_splitkv_gqa(fa, dev):
