@@ -219,7 +219,8 @@ int fa_validate_bwd_varlen(const void* q, const void* k, const void* v, const vo
  * Split-KV forward (no reference counterpart): fa_fwd_gqa_f16's result with
  * each 128-row block's keys cut into num_splits ranges run as separate
  * workgroups, then merged by the LSE combine (fills the GPU when B*H*N/128
- * row blocks are fewer than the CUs and the sequences are long). O within the
+ * row blocks are at most half the CUs, and evens out causal row blocks of
+ * different lengths). O within the
  * forward's tolerance of the unsplit kernel; lse nullable (O only). The
  * workspace (fa_fwd_splitkv_workspace_floats floats, 16-byte aligned) holds
  * the fp32 partials. fa_fwd_splitkv_plan returns the split count the torch
