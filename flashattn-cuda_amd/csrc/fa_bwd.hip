@@ -8,15 +8,21 @@
 // and builds each kernel on v_mfma_f32_32x32x16_f16 with fp32 accumulation:
 //
 //   fa_bwd_di_kernel    D_i = sum_d dO[i][d] * O[i][d] (fp32, stored negated)
-//   fa_bwd_dkdv_kernel  a workgroup owns 128 keys (32 per wave, K and V as
+//   dK/dV body          a workgroup owns 128 keys (32 per wave, K and V as
 //                       register operands) and streams 64-query tiles of Q
-//                       and dO (plus L, D_i) through a double-buffered LDS
-//                       ring: S = Q K^T, dP = dO V^T, P = exp2(S c - L log2e),
+//                       and dO (plus L, D_i) through LDS rings: S = Q K^T,
+//                       dP = dO V^T, P = exp2(S c - L log2e),
 //                       dS = P (dP - D_i), dV^T += dO^T P, dK^T += Q^T dS
-//   fa_bwd_dq_kernel    a workgroup owns 128 queries (32 per wave, Q and dO
+//   dQ body             a workgroup owns 128 queries (32 per wave, Q and dO
 //                       as register operands) and streams 64-key tiles of K
 //                       and V: S^T = K Q^T, dP^T = V dO^T, dS^T as above,
 //                       dQ^T += K^T dS^T
+//
+// The two bodies run as one launch (fa_bwd_fused_kernel) at D = 64 and for
+// causal heads at D = 128, as two (fa_bwd_dkdv_kernel, fa_bwd_dq_kernel) for
+// non-causal heads at D = 128. In each workgroup two wave groups take the
+// two 32-row halves of every tile and run one phase apart, so one wave's
+// MFMAs overlap the other wave's VALU work on every SIMD.
 //
 // P and dS are packed to fp16 straight from the score accumulators as the B
 // operands of the gradient products (the reduction index is permuted the same
@@ -189,355 +195,35 @@ __device__ __forceinline__ void group_reduce(char* smem, int grp, int slot, int 
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV. Workgroup = 4 G waves, 128 keys of one (b, h): wave w owns keys
-// k0 + 32 (w % 4) .. +31 and, with G = 2, query half w / 4 of every tile (the
-// two groups' partial sums are added at the end). Query tiles of 64 rows
-// stream through 2 LDS stages; each stage holds Q and dO twice (row swizzle,
-// transposed swizzle) and 64 floats each of NL and -D_i.
-// ---------------------------------------------------------------------------
-// LDS bytes of the dK/dV body: two stages, or the group reduction's
-// 2 (dK, dV) x DB x 16 floats per lane of 4 waves, whichever is larger.
-template <int D, int G>
-constexpr int dkdv_smem() {
-  constexpr int STAGE = 4 * (kBQ * D * 2) + 2048;   // Qk | Qv | dOk | dOv | NL | -D_i
-  constexpr int RED = (G - 1) * 4 * 2 * (D / 32) * 16 * 64 * 4;
-  return 2 * STAGE > RED ? 2 * STAGE : RED;
-}
-
-template <int D, bool CAUSAL, int G, bool BF16>
-__device__ __forceinline__ void dkdv_body(const f16* __restrict__ Q, const f16* __restrict__ K,
-                                          const f16* __restrict__ V, const f16* __restrict__ dO,
-                                          const float* __restrict__ NL,
-                                          const float* __restrict__ ND, float* __restrict__ dK,
-                                          float* __restrict__ dV, const Geom& geo, int num_kb,
-                                          int total, float c, float scale, int block,
-                                          char* smem /* dkdv_smem<D, G>() bytes, 1 KiB aligned */) {
-  constexpr int TILE = kBQ * D * 2;
-  constexpr int BLOCKS = TILE / 1024;
-  constexpr int KSTEPS = D / 16, DB = D / 32;
-  constexpr int STAGE = 4 * TILE + 2048;       // Qk | Qv | dOk | dOv | NL | -D_i
-  constexpr int WAVES = 4 * G;
-  constexpr int LOADS = 4 * BLOCKS / WAVES;    // tile blocks per wave per stage
-  static_assert(4 * BLOCKS % WAVES == 0, "copy blocks split evenly over the waves");
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kw = wave & 3;
-  const int grp = wave >> 2;
-  const int hi = lane >> 5;
-  const int logical = xcd_remap(block, total, geo.nxcd);
-  const int bh = logical / num_kb;
-  const int kb = logical - bh * num_kb;
-  const int k0 = kb * kBlk;
-
-  const HeadView hv = head_view<D>(geo, bh);
-  const int N = hv.n;
-  if (k0 >= N) return;   // varlen: past this sequence (whole workgroup)
-  const size_t head = hv.q;
-  const int head_bytes = N * D * 2;
-  const char* Qh = reinterpret_cast<const char*>(Q + head);
-  const char* Gh = reinterpret_cast<const char*>(dO + head);
-  const float* Lh = NL + hv.l;
-  const float* Dh = ND + hv.l;   // -D_i
-
-  f16x8 kf[KSTEPS], vf[KSTEPS];   // B operands: K^T and V^T of this wave's keys
-  const size_t kv_head = hv.kv;   // GQA: K/V head of this query head
-  load_row_operand<D>(K + kv_head, N, k0 + 32 * kw, lane, kf);
-  load_row_operand<D>(V + kv_head, N, k0 + 32 * kw, lane, vf);
-  f32x16 acc[2][DB];              // [0] = dV^T, [1] = dK^T (unscaled)
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    acc[0][db] = f32x16{};
-    acc[1][db] = f32x16{};
-  }
-
-  // Block b = i * WAVES + wave of a stage: part b / BLOCKS of {Qk, Qv, dOk,
-  // dOv}, block b % BLOCKS of that tile. The per-lane source offsets are
-  // recomputed at each copy from a lane id the compiler cannot hoist: held
-  // across the loop they are the first registers spilled at D = 128, and a
-  // reload before each copy waits for every copy before it.
-  const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](int t, int st) {
-    const uint32_t base = lds0 + st * STAGE;
-    int ln;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int b = i * WAVES + wave;
-      const int part = b / BLOCKS;
-      uint32_t ko, vo;
-      block_offsets<D>(b % BLOCKS, ln, ko, vo);
-      copy_block<D>(part < 2 ? Qh : Gh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
-                    (part & 1) ? vo : ko);
-    }
-    if (wave == 0) copy_rowvec(Lh, N, t, base + 4 * TILE, ln);
-    if (wave == 1) copy_rowvec(Dh, N, t, base + 4 * TILE + 1024, ln);
-  };
-
-  // One 32-query block qb of the tile at sb: S = Q K^T and dP = dO V^T
-  // (C layout: register r holds query qt0 + 32 qb + 8 (r/4) + 4 hi + r%4,
-  // lane l key l%32), then P, dS and the two gradient products. `mid` runs
-  // once the score products are issued (the next tile's copies go there, so
-  // their issue overlaps the matrix cores).
-  auto body = [&](const char* sb, int qt0, int qb, bool edge, auto mid) {
-    const char* qk = sb;
-    const char* qv = sb + TILE;
-    const char* gk = sb + 2 * TILE;
-    const char* gv = sb + 3 * TILE;
-    const float* ls = reinterpret_cast<const float*>(sb + 4 * TILE);
-    const float* ds = reinterpret_cast<const float*>(sb + 4 * TILE + 1024);
-    f32x16 s = {}, dp = {};
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      s = mma32<BF16>(load_k_frag<D>(qk, qb, kk, lane), kf[kk], s);
-      dp = mma32<BF16>(load_k_frag<D>(gk, qb, kk, lane), vf[kk], dp);
-      // D = 128: bound the operand reads in flight (registers are the limit)
-      if constexpr (D == 128) if (kk % 2 == 1) __builtin_amdgcn_sched_barrier(0);
-    }
-    mid();
-    f32x16 p, g;
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const f32x4 lq = *reinterpret_cast<const f32x4*>(ls + 32 * qb + 8 * r4 + 4 * hi);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p[4 * r4 + e] = exp2_hw(fmaf(s[4 * r4 + e], c, lq[e]));
-    }
-    if (edge) {   // rows past N, and (causal) keys after the row
-      // Register r holds query base + 8 (r/4) + r%4: compare that constant
-      // offset against two per-lane limits. The lane id is read here again
-      // (volatile, so the key index is not held across the loop: at D = 128
-      // that register is one of those the causal instance would spill).
-      int ln;
-      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
-      const int base = qt0 + 32 * qb + 4 * (ln >> 5);
-      const int lim_n = N - base, lim_k = k0 + 32 * kw + (ln & 31) - base;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ro = 8 * (r >> 2) + (r & 3);
-        p[r] = ((ro >= lim_n) || (CAUSAL && ro < lim_k)) ? 0.f : p[r];
-      }
-    }
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const f32x4 dq = *reinterpret_cast<const f32x4*>(ds + 32 * qb + 8 * r4 + 4 * hi);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) g[4 * r4 + e] = p[4 * r4 + e] * (dp[4 * r4 + e] + dq[e]);
-    }
-    // dV^T += dO^T P and dK^T += Q^T dS over the two 16-query k-steps.
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = 2 * qb + h;
-      const f16x8 pb = pack_px<BF16>(p, h);
-      const f16x8 gb = pack_px<BF16>(g, h);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        acc[0][db] = mma32<BF16>(load_v_frag<D>(gv, j, db, lane), pb, acc[0][db]);
-        acc[1][db] = mma32<BF16>(load_v_frag<D>(qv, j, db, lane), gb, acc[1][db]);
-      }
-    }
-  };
-
-  const int n_qt = (N + kBQ - 1) / kBQ;
-  const int t0 = CAUSAL ? k0 / kBQ : 0;   // earlier query tiles see none of these keys
-  if (t0 < n_qt) {
-    issue(t0, 0);
-    wait_vmem();
-    __syncthreads();
-  }
-  for (int t = t0; t < n_qt; ++t) {
-    const int st = (t - t0) & 1;
-    const char* sb = smem + st * STAGE;
-    const int qt0 = t * kBQ;
-    auto prefetch = [&] {
-      if (t + 1 < n_qt) issue(t + 1, st ^ 1);
-    };
-#pragma unroll
-    for (int i = 0; i < 2 / G; ++i) {
-      const int qb = G == 2 ? grp : i;
-      // masking only where a query is past N or precedes one of the keys
-      const bool edge = (qt0 + 32 * qb + 32 > N) ||
-                        (CAUSAL && qt0 + 32 * qb < k0 + 32 * kw + 32);
-      if (i == 0) body(sb, qt0, qb, edge, prefetch);
-      else body(sb, qt0, qb, edge, [] {});
-    }
-    wait_vmem();
-    __syncthreads();
-  }
-  if constexpr (G == 2) group_reduce<2, DB>(smem, grp, kw, lane, acc);
-  if (grp == 0) {
-    store_transposed<D>(dV + head, N, k0 + 32 * kw, lane, acc[0], 1.f);
-    store_transposed<D>(dK + head, N, k0 + 32 * kw, lane, acc[1], scale);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dQ. Workgroup = 4 G waves, 128 queries of one (b, h): wave w owns queries
-// q0 + 32 (w % 4) .. +31 (Q^T and dO^T as register B operands, NL and -D_i as
-// lane constants) and, with G = 2, key half w / 4 of every tile. Key tiles of
-// 64 rows stream through 2 LDS stages, each holding K twice (row swizzle,
-// transposed swizzle) and V once (row swizzle).
-// ---------------------------------------------------------------------------
-// LDS bytes of the dQ body: two stages, or the group reduction's DB x 16
-// floats per lane of 4 waves, whichever is larger.
-template <int D, int G>
-constexpr int dq_smem() {
-  constexpr int STAGE = 3 * (kBQ * D * 2);    // Kk | Kv | Vk
-  constexpr int RED = (G - 1) * 4 * (D / 32) * 16 * 64 * 4;
-  return 2 * STAGE > RED ? 2 * STAGE : RED;
-}
-
-template <int D, bool CAUSAL, int G, bool BF16>
-__device__ __forceinline__ void dq_body(const f16* __restrict__ Q, const f16* __restrict__ K,
-                                        const f16* __restrict__ V, const f16* __restrict__ dO,
-                                        const float* __restrict__ NL,
-                                        const float* __restrict__ ND, float* __restrict__ dQ,
-                                        const Geom& geo, int num_qb, int total, float c,
-                                        float scale, int block,
-                                        char* smem /* dq_smem<D, G>() bytes, 1 KiB aligned */) {
-  constexpr int TILE = kBQ * D * 2;
-  constexpr int BLOCKS = TILE / 1024;
-  constexpr int KSTEPS = D / 16, DB = D / 32;
-  constexpr int STAGE = 3 * TILE;              // Kk | Kv | Vk
-  constexpr int NBLK = 3 * BLOCKS;
-  constexpr int WAVES = 4 * G;
-  constexpr int LOADS = (NBLK + WAVES - 1) / WAVES;   // tile blocks per wave per stage
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int qw = wave & 3;
-  const int grp = wave >> 2;
-  const int hi = lane >> 5;
-  const int logical = xcd_remap(block, total, geo.nxcd);
-  const int bh = logical / num_qb;
-  int qb = logical - bh * num_qb;
-  if (CAUSAL) qb = num_qb - 1 - qb;   // longest rows first
-  const int q0 = qb * kBlk;
-  const int query = q0 + 32 * qw + (lane & 31);
-
-  const HeadView hv = head_view<D>(geo, bh);
-  const int N = hv.n;
-  if (q0 >= N) return;   // varlen: past this sequence (whole workgroup)
-  const size_t head = hv.q;
-  const int head_bytes = N * D * 2;
-  const size_t kv_head = hv.kv;   // GQA: K/V head of this query head
-  const char* Kh = reinterpret_cast<const char*>(K + kv_head);
-  const char* Vh = reinterpret_cast<const char*>(V + kv_head);
-
-  f16x8 qf[KSTEPS], gf[KSTEPS];   // B operands: Q^T and dO^T of this wave's queries
-  load_row_operand<D>(Q + head, N, q0 + 32 * qw, lane, qf);
-  load_row_operand<D>(dO + head, N, q0 + 32 * qw, lane, gf);
-  const bool row_ok = query < N;
-  const float nl = row_ok ? NL[hv.l + query] : 0.f;
-  const float dq_i = row_ok ? ND[hv.l + query] : 0.f;   // -D_i
-  f32x16 acc[1][DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) acc[0][db] = f32x16{};
-
-  const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](int t, int st) {   // offsets recomputed per copy (see the dK/dV body)
-    const uint32_t base = lds0 + st * STAGE;
-    int ln;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int b = i * WAVES + wave;
-      if (b < NBLK) {   // wave-uniform
-        const int part = b / BLOCKS;
-        uint32_t ko, vo;
-        block_offsets<D>(b % BLOCKS, ln, ko, vo);
-        copy_block<D>(part < 2 ? Kh : Vh, head_bytes, t, base + part * TILE + (b % BLOCKS) * 1024,
-                      part == 1 ? vo : ko);
-      }
-    }
-  };
-
-  // One 32-key half of the tile at kt: S^T = K Q^T and dP^T = V dO^T
-  // (register r holds key kt0 + 32 half + 8 (r/4) + 4 hi + r%4, lane l query
-  // l%32), then dS^T and dQ^T += K^T dS^T. `mid` runs once the score
-  // products are issued.
-  auto body = [&](const char* kt, int kt0, int half, bool edge, auto mid) {
-    const char* kk_t = kt;
-    const char* kv_t = kt + TILE;
-    const char* vk_t = kt + 2 * TILE;
-    f32x16 s = {}, dp = {};
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      s = mma32<BF16>(load_k_frag<D>(kk_t, half, kk, lane), qf[kk], s);
-      dp = mma32<BF16>(load_k_frag<D>(vk_t, half, kk, lane), gf[kk], dp);
-    }
-    mid();
-    f32x16 p;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = exp2_hw(fmaf(s[r], c, nl));
-    if (edge) {   // keys past N, rows past N, and (causal) keys after the row
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kidx = kt0 + 32 * half + 8 * (r >> 2) + 4 * hi + (r & 3);
-        p[r] = ((kidx >= N) || (CAUSAL && kidx > query) || !row_ok) ? 0.f : p[r];
-      }
-    }
-    f32x16 g;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) g[r] = p[r] * (dp[r] + dq_i);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = 2 * half + h;
-      const f16x8 gb = pack_px<BF16>(g, h);
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        acc[0][db] = mma32<BF16>(load_v_frag<D>(kv_t, j, db, lane), gb, acc[0][db]);
-    }
-  };
-
-  const int kv_end = CAUSAL ? min(N, q0 + kBlk) : N;
-  const int n_kt = (kv_end + kBQ - 1) / kBQ;
-  // rows past N (last block only) and, causal, keys after the wave's first query
-  const bool rows_edge = q0 + 32 * qw + 32 > N;
-  issue(0, 0);
-  wait_vmem();
-  __syncthreads();
-  for (int t = 0; t < n_kt; ++t) {
-    const int st = t & 1;
-    const char* kt = smem + st * STAGE;
-    const int kt0 = t * kBQ;
-    auto prefetch = [&] {
-      if (t + 1 < n_kt) issue(t + 1, st ^ 1);
-    };
-#pragma unroll
-    for (int i = 0; i < 2 / G; ++i) {
-      const int half = G == 2 ? grp : i;
-      const bool edge = rows_edge || (kt0 + 32 * half + 32 > N) ||
-                        (CAUSAL && kt0 + 32 * half + 31 > q0 + 32 * qw);
-      if (i == 0) body(kt, kt0, half, edge, prefetch);
-      else body(kt, kt0, half, edge, [] {});
-    }
-    wait_vmem();
-    __syncthreads();
-  }
-  if constexpr (G == 2) group_reduce<1, DB>(smem, grp, qw, lane, acc);
-  if (grp == 0) store_transposed<D>(dQ + head, N, q0 + 32 * qw, lane, acc[0], scale);
-}
-
-// ---------------------------------------------------------------------------
-// Ping-pong forms of the two bodies (D = 64, 8 waves): the two wave groups of
-// a workgroup hold the same keys (dK/dV) or queries (dQ), each takes one
-// 32-row half of every tile, and they run one phase apart. Each tile's work
-// splits into the score products A (S and dP MFMAs), the VALU part B (P,
-// dS, packed as B operands) and the gradient products C; a group's matrix
-// phase M(j) issues C of its tile j - 1 and A of tile j, its softmax phase
-// S(j) runs B of tile j. In every phase one group is in M and the other in
-// S, so each SIMD overlaps one wave's MFMAs with the other's VALU work (the
-// lockstep bodies above run the two waves' MFMAs and VALU at the same time):
+// dK/dV and dQ bodies (8 waves). A dK/dV workgroup owns 128 keys of one
+// (b, h): wave w holds K^T and V^T of keys k0 + 32 (w % 4) .. +31 as register
+// B operands, and 64-query tiles of Q and dO stream through LDS, each stored
+// twice (row swizzle for the score products, transposed swizzle for the
+// gradient products), with 64 floats each of NL and -D_i. A dQ workgroup
+// owns 128 queries the same way (Q^T and dO^T as register operands, NL and
+// -D_i lane constants) and streams 64-key tiles of K (twice) and V.
+//
+// The two wave groups (waves 0-3 and 4-7) hold the same keys (dK/dV) or
+// queries (dQ), each takes one 32-row half of every tile, their partial sums
+// are added through LDS at the end (group_reduce), and they run one phase
+// apart. Each tile's work splits into the score products A (S and dP
+// MFMAs), the VALU part B (P, dS, packed as B operands) and the gradient
+// products C; a group's matrix phase M(j) issues C of its tile j - 1 and A
+// of tile j, its softmax phase S(j) runs B of tile j. In every phase one
+// group is in M and the other in S, so each SIMD overlaps one wave's MFMAs
+// with the other's VALU work:
 //
 //   phase      2j          2j+1        ...   2T          2T+1
 //   group 0    M(j)        S(j)              C(T-1)      -
 //   group 1    S(j-1)      M(j)              S(T-1)      C(T-1)
 //
-// A group reads only its own 32-row half of every tile (rows 32 g .. +31 of
-// each part are its 1 KiB blocks 4 g .. 4 g + 3 in both swizzles), so it
-// copies only that half, and the row vectors into slots of its own: the
-// groups share no staged data, and the barriers keep them one phase apart
-// and sync each group's four waves on their copies. Tile j's stage is read
+// A group reads only its own 32-row half of every tile, so it copies only
+// that half, and the row vectors into slots of its own: the groups share no
+// staged data, and the barriers keep them one phase apart and sync each
+// group's four waves on their copies.
+//
+// D = 64 (rows 32 g .. +31 of each part are its 1 KiB blocks 4 g .. 4 g + 3
+// in both swizzles): tile j's stage is read
 // from S(j - 1), which loads tile j's A operands into registers (M(j) then
 // issues its score products without LDS waits), to M(j + 1), which reads its
 // C operands. S(j) starts the copies of tile j + 3 into the stage of tile
@@ -936,40 +622,480 @@ __device__ __forceinline__ void dq_body_pp(const f16* __restrict__ Q, const f16*
   if (grp == 0) store_transposed<D>(dQ + head, N, q0 + 32 * qw, lane, acc[0], scale);
 }
 
-// GQA: dK, dV of KV head hk = sum over its `group` query heads of the
-// per-query-head partials (fp32 [B*H, N*D] -> [B*Hkv, N*D]), four floats per
-// thread.
-template <int D, bool CAUSAL, int G, bool BF16>
-__global__ void __launch_bounds__(256 * G)
+// ---------------------------------------------------------------------------
+// D = 128. The phases are those of the D = 64 forms (M(j): C of tile j - 1,
+// then A of tile j; S(j): B of tile j; the two groups one phase apart),
+// fitted to D = 128's budgets:
+//   * registers: the score products' A operands are read from LDS inside
+//     the M phase (not prefetched into registers), and the M phase runs all
+//     of C(j - 1) before A(j), so the packed P and dS of tile j - 1 are dead
+//     before S and dP of tile j are live: the dK/dV body fits the 256 VGPRs
+//     of two waves per SIMD without spilling (K^T, V^T and the two
+//     accumulators alone take 192);
+//   * LDS: the parts of a tile are freed at different times (the row-swizzled
+//     A parts after M(j), the row vectors after S(j), the transposed C parts
+//     after M(j + 1)), so each part has its own ring of slots and S(j) starts
+//     A of tile j + 2, C of tile j + 1 and the row vectors of tile j + 2,
+//     each into the slot its last reader has just left: two A slots, two C
+//     slots and three row-vector slots (131 KiB at D = 128 for dK/dV) give
+//     every copy two phases to land, issued from the VALU phase.
+// A group copies and reads only its own 32-row half of every part (rows
+// 32 g .. +31 are 1 KiB blocks 8 g .. 8 g + 7 in both swizzles).
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr int dkdv_pp128_smem() {
+  constexpr int TILE = kBQ * D * 2;
+  constexpr int RING = 2 * (2 * TILE) + 2 * (2 * TILE) + 3 * 1024;
+  constexpr int RED = 4 * 2 * (D / 32) * 16 * 64 * 4;
+  return RING > RED ? RING : RED;
+}
+
+template <int D>
+constexpr int dq_pp128_smem() {
+  constexpr int TILE = kBQ * D * 2;
+  constexpr int RING = 2 * (2 * TILE) + 2 * TILE;
+  constexpr int RED = 4 * (D / 32) * 16 * 64 * 4;
+  return RING > RED ? RING : RED;
+}
+
+template <int D, bool CAUSAL, bool BF16>
+__device__ __forceinline__ void dkdv_body_pp128(const f16* __restrict__ Q,
+                                                const f16* __restrict__ K,
+                                                const f16* __restrict__ V,
+                                                const f16* __restrict__ dO,
+                                                const float* __restrict__ NL,
+                                                const float* __restrict__ ND,
+                                                float* __restrict__ dK, float* __restrict__ dV,
+                                                const Geom& geo, int num_kb, int total, float c,
+                                                float scale, int block,
+                                                char* smem /* dkdv_pp128_smem<D>() bytes */) {
+  static_assert(D == 128, "a 32-row half of a tile is 8 blocks");
+  constexpr int TILE = kBQ * D * 2;
+  constexpr int BLOCKS = TILE / 1024;
+  constexpr int OWN = BLOCKS / 2;              // blocks of a 32-row half
+  constexpr int PER = OWN / 2;                 // blocks per wave of one part's half
+  constexpr int KSTEPS = D / 16, DB = D / 32;
+  constexpr int SLOT = 2 * TILE;               // A slot: Qk | dOk; C slot: Qv | dOv
+  constexpr int C0 = 2 * SLOT;                 // C ring after the A ring
+  constexpr int R0 = 4 * SLOT;                 // row vectors: group g L at +512 g, -D_i +256
+  static_assert(R0 + 3 * 1024 <= dkdv_pp128_smem<D>() && dkdv_pp128_smem<D>() <= 160 * 1024,
+                "ring inside the buffer, LDS");
+  static_assert(2 * KSTEPS == 2 * 2 * DB, "C and A take the same number of steps");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kw = wave & 3;
+  const int grp = wave >> 2;                   // also this group's query half of a tile
+  const int qb = grp;
+  const int hi = lane >> 5;
+  const int logical = xcd_remap(block, total, geo.nxcd);
+  const int bh = logical / num_kb;
+  const int kb = logical - bh * num_kb;
+  const int k0 = kb * kBlk;
+
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (k0 >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
+  const int head_bytes = N * D * 2;
+  const char* Qh = reinterpret_cast<const char*>(Q + head);
+  const char* Gh = reinterpret_cast<const char*>(dO + head);
+  const float* Lh = NL + hv.l;
+  const float* Dh = ND + hv.l;   // -D_i
+
+  f16x8 kf[KSTEPS], vf[KSTEPS];   // B operands: K^T and V^T of this wave's keys
+  load_row_operand<D>(K + hv.kv, N, k0 + 32 * kw, lane, kf);
+  load_row_operand<D>(V + hv.kv, N, k0 + 32 * kw, lane, vf);
+  f32x16 acc[2][DB];              // [0] = dV^T, [1] = dK^T (unscaled)
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    acc[0][db] = f32x16{};
+    acc[1][db] = f32x16{};
+  }
+
+  const int n_qt = (N + kBQ - 1) / kBQ;
+  const int t0 = CAUSAL ? k0 / kBQ : 0;   // earlier query tiles see none of these keys
+  const int T = n_qt - t0;                 // tiles of this workgroup (>= 1)
+
+  const uint32_t lds0 = lds_addr(smem);
+  // Wave kw copies blocks 8 grp + 4 (kw & 1) .. +3 of part kw >> 1 (Q or dO)
+  // of a ring; the per-lane offsets are recomputed per copy (volatile lane
+  // id: held across the loop they would take registers the body needs).
+  auto issue_part = [&](int t, uint32_t base, bool vsw) {
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const char* src = kw < 2 ? Qh : Gh;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int b = OWN * grp + PER * (kw & 1) + i;
+      uint32_t ko, vo;
+      block_offsets<D>(b, ln, ko, vo);
+      copy_block<D>(src, head_bytes, t, base + (kw >> 1) * TILE + b * 1024, vsw ? vo : ko);
+    }
+  };
+  auto issue_a = [&](int j) {   // A parts and row vectors of relative tile j
+    issue_part(t0 + j, lds0 + (j & 1) * SLOT, false);
+    const uint32_t rv = lds0 + R0 + (j % 3) * 1024 + 512 * grp;
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    if (kw == 0) copy_rowvec(Lh, N, t0 + j, rv, ln);
+    if (kw == 1) copy_rowvec(Dh, N, t0 + j, rv + 256, ln);
+  };
+  auto issue_c = [&](int j) { issue_part(t0 + j, lds0 + C0 + (j & 1) * SLOT, true); };
+  // Copies issued by this wave in one S phase: A (PER, + 1 row vector for
+  // waves 0 and 1) and C (PER). The end of S(j) leaves S(j)'s copies in
+  // flight and waits for the rest.
+  auto wait_for = [&](bool a, bool cc) {
+    if (a && cc) {
+      if (kw < 2) wait_vmcnt<2 * PER + 1>();
+      else wait_vmcnt<2 * PER>();
+    } else if (a) {
+      if (kw < 2) wait_vmcnt<PER + 1>();
+      else wait_vmcnt<PER>();
+    } else if (cc) {
+      wait_vmcnt<PER>();
+    } else {
+      wait_vmem();
+    }
+  };
+  issue_a(0);
+  issue_c(0);
+  if (T > 1) issue_a(1);
+  wait_vmem();
+  __syncthreads();
+
+  f32x16 s = {}, dp = {};   // this wave's scores of its current tile
+  f16x8 pb[2], gb[2];       // its packed P and dS (B operands of the two k-steps)
+  // M phase of relative tile j: C of tile j - 1 (dV^T += dO^T P, dK^T += Q^T
+  // dS; step x: k-step x / DB, d-block x % DB), then A of tile j (S = Q K^T,
+  // dP = dO V^T; step x: k-step x). Operands two steps ahead.
+  auto mphase = [&](int j, auto with_c, auto with_a) {
+    constexpr bool WC = decltype(with_c)::value, WA = decltype(with_a)::value;
+    constexpr int X0 = WC ? 0 : KSTEPS, X1 = WA ? 2 * KSTEPS : KSTEPS;
+    const char* sc = smem + C0 + ((j + 1) & 1) * SLOT;   // C slot of tile j - 1
+    const char* sa = smem + (j & 1) * SLOT;              // A slot of tile j
+    f16x8 f[2 * KSTEPS][2];
+    auto load = [&](auto xi) {
+      constexpr int x = decltype(xi)::value;
+      if constexpr (x < KSTEPS) {
+        const int jj = 2 * qb + x / DB;
+        f[x][0] = load_v_frag<D>(sc + TILE, jj, x % DB, lane);   // dO^T
+        f[x][1] = load_v_frag<D>(sc, jj, x % DB, lane);          // Q^T
+      } else {
+        f[x][0] = load_k_frag<D>(sa, qb, x - KSTEPS, lane);          // Q rows
+        f[x][1] = load_k_frag<D>(sa + TILE, qb, x - KSTEPS, lane);   // dO rows
+      }
+    };
+    // Operands two steps ahead within each part; A's first two are loaded
+    // where A starts, once C's last operands are consumed (loading them
+    // during C measured 2 % slower at config 3).
+    auto ahead = [&](auto xi) {
+      constexpr int x = decltype(xi)::value;
+      if constexpr (x < X1 && (x < KSTEPS || x >= KSTEPS + 2 || !WC)) load(xi);
+    };
+    static_for<X0, X0 + 2>(load);   // X1 - X0 >= KSTEPS
+    static_for<X0, X1>([&](auto xi) {
+      constexpr int x = decltype(xi)::value;
+      if constexpr (WC && WA && x == KSTEPS) static_for<KSTEPS, KSTEPS + 2>(load);
+      ahead(std::integral_constant<int, x + 2>{});
+      if constexpr (x < KSTEPS) {
+        acc[0][x % DB] = mma32<BF16>(f[x][0], pb[x / DB], acc[0][x % DB]);
+        acc[1][x % DB] = mma32<BF16>(f[x][1], gb[x / DB], acc[1][x % DB]);
+      } else {
+        constexpr int kk = x - KSTEPS;
+        s = mma32<BF16>(f[x][0], kf[kk], kk == 0 ? f32x16{} : s);
+        dp = mma32<BF16>(f[x][1], vf[kk], kk == 0 ? f32x16{} : dp);
+      }
+      if constexpr (x + 1 == KSTEPS) __builtin_amdgcn_sched_barrier(0);   // C before A
+    });
+    __builtin_amdgcn_sched_barrier(0);   // keep every product in this phase
+  };
+  // S phase of relative tile j: the copies of A(j + 2), C(j + 1) and the row
+  // vectors of j + 2, then P and dS into pb, gb; at the end, the wait for
+  // the copies of S(j - 1) (A(j + 1), C(j): M(j + 1) reads them).
+  auto sphase = [&](int j) {
+    const bool ca = j + 2 < T, cc = j + 1 < T;
+    if (cc) issue_c(j + 1);
+    if (ca) issue_a(j + 2);
+    const int qt0 = (t0 + j) * kBQ;
+    const float* ls = reinterpret_cast<const float*>(smem + R0 + (j % 3) * 1024 + 512 * grp);
+    const float* nds = ls + 64;
+    f32x16 p, g;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4 lq = *reinterpret_cast<const f32x4*>(ls + 32 * qb + 8 * r4 + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[4 * r4 + e] = exp2_hw(fmaf(s[4 * r4 + e], c, lq[e]));
+    }
+    const bool edge = (qt0 + 32 * qb + 32 > N) || (CAUSAL && qt0 + 32 * qb < k0 + 32 * kw + 32);
+    if (edge) {   // rows past N, and (causal) keys after the row
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      const int base = qt0 + 32 * qb + 4 * (ln >> 5);
+      const int lim_n = N - base, lim_k = k0 + 32 * kw + (ln & 31) - base;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ro = 8 * (r >> 2) + (r & 3);
+        p[r] = ((ro >= lim_n) || (CAUSAL && ro < lim_k)) ? 0.f : p[r];
+      }
+    }
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4 dq = *reinterpret_cast<const f32x4*>(nds + 32 * qb + 8 * r4 + 4 * hi);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g[4 * r4 + e] = p[4 * r4 + e] * (dp[4 * r4 + e] + dq[e]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      pb[h] = pack_px<BF16>(p, h);
+      gb[h] = pack_px<BF16>(g, h);
+    }
+    wait_for(ca, cc);
+  };
+  auto pin_s = [&] { asm volatile("" : "+v"(s), "+v"(dp)); };
+  auto pin_p = [&] { asm volatile("" : "+v"(pb[0]), "+v"(pb[1]), "+v"(gb[0]), "+v"(gb[1])); };
+
+  using BT = std::true_type;
+  using BF = std::false_type;
+  if (grp == 1) __syncthreads();   // phase 0: group 1 waits
+  mphase(0, BF{}, BT{});
+  __syncthreads();
+  pin_s();
+  sphase(0);
+  pin_p();
+  __syncthreads();
+  for (int j = 1; j < T; ++j) {
+    mphase(j, BT{}, BT{});
+    __syncthreads();
+    pin_s();
+    sphase(j);
+    pin_p();
+    __syncthreads();
+  }
+  mphase(T, BT{}, BF{});   // C of the last tile
+  __syncthreads();
+  if (grp == 0) __syncthreads();   // phase 2T + 1: group 0 waits
+  int ln;   // the lane id again (not held across the loop)
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+  group_reduce<2, DB>(smem, grp, kw, ln, acc);
+  if (grp == 0) {
+    store_transposed<D>(dV + head, N, k0 + 32 * kw, ln, acc[0], 1.f);
+    store_transposed<D>(dK + head, N, k0 + 32 * kw, ln, acc[1], scale);
+  }
+}
+
+template <int D, bool CAUSAL, bool BF16>
+__device__ __forceinline__ void dq_body_pp128(const f16* __restrict__ Q, const f16* __restrict__ K,
+                                              const f16* __restrict__ V,
+                                              const f16* __restrict__ dO,
+                                              const float* __restrict__ NL,
+                                              const float* __restrict__ ND, float* __restrict__ dQ,
+                                              const Geom& geo, int num_qb, int total, float c,
+                                              float scale, int block,
+                                              char* smem /* dq_pp128_smem<D>() bytes */) {
+  static_assert(D == 128, "a 32-row half of a tile is 8 blocks");
+  constexpr int TILE = kBQ * D * 2;
+  constexpr int BLOCKS = TILE / 1024;
+  constexpr int OWN = BLOCKS / 2;              // blocks of a 32-row half
+  constexpr int PA = OWN / 2, PC = OWN / 4;    // blocks per wave: A parts, C part
+  constexpr int KSTEPS = D / 16, DB = D / 32;
+  constexpr int SLOT = 2 * TILE;               // A slot: Kk | Vk
+  constexpr int C0 = 2 * SLOT;                 // C slots (Kv), TILE bytes each
+  static_assert(C0 + 2 * TILE <= dq_pp128_smem<D>() && dq_pp128_smem<D>() <= 160 * 1024 &&
+                OWN % 4 == 0, "ring inside the buffer, LDS, copy split");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qw = wave & 3;
+  const int grp = wave >> 2;                   // also this group's key half of a tile
+  const int half = grp;
+  const int hi = lane >> 5;
+  const int logical = xcd_remap(block, total, geo.nxcd);
+  const int bh = logical / num_qb;
+  int qblk = logical - bh * num_qb;
+  if (CAUSAL) qblk = num_qb - 1 - qblk;   // longest rows first
+  const int q0 = qblk * kBlk;
+  const int query = q0 + 32 * qw + (lane & 31);
+
+  const HeadView hv = head_view<D>(geo, bh);
+  const int N = hv.n;
+  if (q0 >= N) return;   // varlen: past this sequence (whole workgroup)
+  const size_t head = hv.q;
+  const int head_bytes = N * D * 2;
+  const char* Kh = reinterpret_cast<const char*>(K + hv.kv);
+  const char* Vh = reinterpret_cast<const char*>(V + hv.kv);
+
+  f16x8 qf[KSTEPS], gf[KSTEPS];   // B operands: Q^T and dO^T of this wave's queries
+  load_row_operand<D>(Q + head, N, q0 + 32 * qw, lane, qf);
+  load_row_operand<D>(dO + head, N, q0 + 32 * qw, lane, gf);
+  const bool row_ok = query < N;
+  const float nl = row_ok ? NL[hv.l + query] : 0.f;
+  const float dq_i = row_ok ? ND[hv.l + query] : 0.f;   // -D_i
+  f32x16 acc[1][DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[0][db] = f32x16{};
+
+  const int kv_end = CAUSAL ? min(N, q0 + kBlk) : N;
+  const int T = (kv_end + kBQ - 1) / kBQ;   // >= 1
+  // rows past N (last block only) and, causal, keys after the wave's first query
+  const bool rows_edge = q0 + 32 * qw + 32 > N;
+
+  const uint32_t lds0 = lds_addr(smem);
+  // A parts (Kk, Vk): wave qw copies blocks 8 grp + 4 (qw & 1) .. +3 of part
+  // qw >> 1; C part (Kv): blocks 8 grp + 2 qw .. +1.
+  auto issue_a = [&](int j) {
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const uint32_t base = lds0 + (j & 1) * SLOT + (qw >> 1) * TILE;
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+      const int b = OWN * grp + PA * (qw & 1) + i;
+      uint32_t ko, vo;
+      block_offsets<D>(b, ln, ko, vo);
+      copy_block<D>(qw < 2 ? Kh : Vh, head_bytes, j, base + b * 1024, ko);
+    }
+  };
+  auto issue_c = [&](int j) {
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const uint32_t base = lds0 + C0 + (j & 1) * TILE;
+#pragma unroll
+    for (int i = 0; i < PC; ++i) {
+      const int b = OWN * grp + PC * qw + i;
+      uint32_t ko, vo;
+      block_offsets<D>(b, ln, ko, vo);
+      copy_block<D>(Kh, head_bytes, j, base + b * 1024, vo);
+    }
+  };
+  auto wait_for = [&](bool a, bool cc) {
+    if (a && cc) wait_vmcnt<PA + PC>();
+    else if (a) wait_vmcnt<PA>();
+    else if (cc) wait_vmcnt<PC>();
+    else wait_vmem();
+  };
+  issue_a(0);
+  issue_c(0);
+  if (T > 1) issue_a(1);
+  wait_vmem();
+  __syncthreads();
+
+  f32x16 s = {}, dp = {};
+  f16x8 gb[2];
+  // M phase of tile j: C of tile j - 1 (dQ^T += K^T dS^T; step x: k-step
+  // x / DB, d-block x % DB), then A of tile j (S^T = K Q^T, dP^T = V dO^T).
+  auto mphase = [&](int j, auto with_c, auto with_a) {
+    constexpr bool WC = decltype(with_c)::value, WA = decltype(with_a)::value;
+    constexpr int CX = 2 * DB;   // C steps
+    constexpr int X0 = WC ? 0 : CX, X1 = WA ? CX + KSTEPS : CX;
+    const char* sc = smem + C0 + ((j + 1) & 1) * TILE;   // C slot of tile j - 1
+    const char* sa = smem + (j & 1) * SLOT;              // A slot of tile j
+    f16x8 f[CX + KSTEPS][2];
+    auto load = [&](auto xi) {
+      constexpr int x = decltype(xi)::value;
+      if constexpr (x < CX) {
+        f[x][0] = load_v_frag<D>(sc, 2 * half + x / DB, x % DB, lane);   // K^T
+      } else {
+        f[x][0] = load_k_frag<D>(sa, half, x - CX, lane);          // K rows
+        f[x][1] = load_k_frag<D>(sa + TILE, half, x - CX, lane);   // V rows
+      }
+    };
+    static_for<X0, X0 + 2 < X1 ? X0 + 2 : X1>(load);
+    static_for<X0, X1>([&](auto xi) {
+      constexpr int x = decltype(xi)::value;
+      if constexpr (x + 2 < X1) load(std::integral_constant<int, x + 2>{});
+      if constexpr (x < CX) {
+        acc[0][x % DB] = mma32<BF16>(f[x][0], gb[x / DB], acc[0][x % DB]);
+      } else {
+        constexpr int kk = x - CX;
+        s = mma32<BF16>(f[x][0], qf[kk], kk == 0 ? f32x16{} : s);
+        dp = mma32<BF16>(f[x][1], gf[kk], kk == 0 ? f32x16{} : dp);
+      }
+      if constexpr (x + 1 == CX) __builtin_amdgcn_sched_barrier(0);   // C before A
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto sphase = [&](int j) {
+    const bool ca = j + 2 < T, cc = j + 1 < T;
+    if (cc) issue_c(j + 1);
+    if (ca) issue_a(j + 2);
+    const int kt0 = j * kBQ;
+    f32x16 p;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = exp2_hw(fmaf(s[r], c, nl));
+    const bool edge = rows_edge || (kt0 + 32 * half + 32 > N) ||
+                      (CAUSAL && kt0 + 32 * half + 31 > q0 + 32 * qw);
+    if (edge) {   // keys past N, rows past N, and (causal) keys after the row
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kidx = kt0 + 32 * half + 8 * (r >> 2) + 4 * hi + (r & 3);
+        p[r] = ((kidx >= N) || (CAUSAL && kidx > query) || !row_ok) ? 0.f : p[r];
+      }
+    }
+    f32x16 g;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) g[r] = p[r] * (dp[r] + dq_i);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) gb[h] = pack_px<BF16>(g, h);
+    wait_for(ca, cc);
+  };
+  auto pin_s = [&] { asm volatile("" : "+v"(s), "+v"(dp)); };
+  auto pin_p = [&] { asm volatile("" : "+v"(gb[0]), "+v"(gb[1])); };
+
+  using BT = std::true_type;
+  using BF = std::false_type;
+  if (grp == 1) __syncthreads();   // phase 0: group 1 waits
+  mphase(0, BF{}, BT{});
+  __syncthreads();
+  pin_s();
+  sphase(0);
+  pin_p();
+  __syncthreads();
+  for (int j = 1; j < T; ++j) {
+    mphase(j, BT{}, BT{});
+    __syncthreads();
+    pin_s();
+    sphase(j);
+    pin_p();
+    __syncthreads();
+  }
+  mphase(T, BT{}, BF{});   // C of the last tile
+  __syncthreads();
+  if (grp == 0) __syncthreads();   // phase 2T + 1: group 0 waits
+  group_reduce<1, DB>(smem, grp, qw, lane, acc);
+  if (grp == 0) store_transposed<D>(dQ + head, N, q0 + 32 * qw, lane, acc[0], scale);
+}
+
+// Non-causal D = 128 runs the two bodies as two launches (see launch_bwd).
+template <bool CAUSAL, bool BF16>
+__global__ void __launch_bounds__(512)
 fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                    const f16* __restrict__ V, const f16* __restrict__ dO,
                    const float* __restrict__ NL, const float* __restrict__ ND,
                    float* __restrict__ dK, float* __restrict__ dV, Geom geo, int num_kb,
                    int total, float c, float scale) {
-  __shared__ __attribute__((aligned(1024))) char smem[dkdv_smem<D, G>()];
-  dkdv_body<D, CAUSAL, G, BF16>(Q, K, V, dO, NL, ND, dK, dV, geo, num_kb, total, c, scale,
-                                (int)blockIdx.x, smem);
+  __shared__ __attribute__((aligned(1024))) char smem[dkdv_pp128_smem<128>()];
+  dkdv_body_pp128<128, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dK, dV, geo, num_kb, total, c, scale,
+                                     (int)blockIdx.x, smem);
 }
 
-template <int D, bool CAUSAL, int G, bool BF16>
-__global__ void __launch_bounds__(256 * G)
+template <bool CAUSAL, bool BF16>
+__global__ void __launch_bounds__(512)
 fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                  const f16* __restrict__ V, const f16* __restrict__ dO,
                  const float* __restrict__ NL, const float* __restrict__ ND,
                  float* __restrict__ dQ, Geom geo, int num_qb, int total, float c,
                  float scale) {
-  __shared__ __attribute__((aligned(1024))) char smem[dq_smem<D, G>()];
-  dq_body<D, CAUSAL, G, BF16>(Q, K, V, dO, NL, ND, dQ, geo, num_qb, total, c, scale,
-                              (int)blockIdx.x, smem);
+  __shared__ __attribute__((aligned(1024))) char smem[dq_pp128_smem<128>()];
+  dq_body_pp128<128, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dQ, geo, num_qb, total, c, scale,
+                                   (int)blockIdx.x, smem);
 }
 
 // dK/dV and dQ in one launch (both bodies take 8 waves and share one LDS
 // buffer): blocks [0, total) are the dK/dV kernel's, [total, 2 total) the dQ
-// kernel's. Each
-// half is dispatched longest unit first, so a CU that finished a short dK/dV
-// unit (late keys of a causal head) picks up a long dQ unit: the causal
-// triangle's two halves even out across the CUs instead of each kernel
-// waiting for its own longest unit.
+// kernel's. Each half is dispatched longest unit first, so a CU that
+// finished a short dK/dV unit (late keys of a causal head) picks up a long
+// dQ unit: the causal triangle's two halves even out across the CUs instead
+// of each kernel waiting for its own longest unit.
 template <int D, bool CAUSAL, bool BF16>
 __global__ void __launch_bounds__(512)
 fa_bwd_fused_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
@@ -977,32 +1103,33 @@ fa_bwd_fused_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                     const float* __restrict__ NL, const float* __restrict__ ND,
                     float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ dQ,
                     Geom geo, int nb, int total, float c, float scale) {
-  // One LDS buffer serves whichever body this workgroup runs. D = 64 runs the
-  // ping-pong bodies (their 4-stage rings fit the LDS only there).
-  constexpr bool PP = D == 64;
-  constexpr int SK = PP ? dkdv_pp_smem<D>() : dkdv_smem<D, 2>();
-  constexpr int SQ = PP ? dq_pp_smem<D>() : dq_smem<D, 2>();
+  // One LDS buffer serves whichever body this workgroup runs.
+  constexpr int SK = D == 64 ? dkdv_pp_smem<D>() : dkdv_pp128_smem<D>();
+  constexpr int SQ = D == 64 ? dq_pp_smem<D>() : dq_pp128_smem<D>();
   __shared__ __attribute__((aligned(1024))) char smem[SK > SQ ? SK : SQ];
   const int blk = (int)blockIdx.x;
   if (blk < total) {
-    if constexpr (PP) {
+    if constexpr (D == 64) {
       dkdv_body_pp<D, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dK, dV, geo, nb, total, c, scale, blk,
                                     smem);
     } else {
-      dkdv_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, ND, dK, dV, geo, nb, total, c, scale, blk,
-                                    smem);
+      dkdv_body_pp128<D, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dK, dV, geo, nb, total, c, scale,
+                                       blk, smem);
     }
   } else {
-    if constexpr (PP) {
+    if constexpr (D == 64) {
       dq_body_pp<D, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dQ, geo, nb, total, c, scale, blk - total,
                                   smem);
     } else {
-      dq_body<D, CAUSAL, 2, BF16>(Q, K, V, dO, NL, ND, dQ, geo, nb, total, c, scale, blk - total,
-                                  smem);
+      dq_body_pp128<D, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dQ, geo, nb, total, c, scale,
+                                     blk - total, smem);
     }
   }
 }
 
+// GQA: dK, dV of KV head hk = sum over its `group` query heads of the
+// per-query-head partials (fp32 [B*H, N*D] -> [B*Hkv, N*D]), four floats per
+// thread.
 __global__ void __launch_bounds__(256)
 fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out, int64_t head_elems,
                         int64_t kv_heads, int group) {
@@ -1017,18 +1144,6 @@ fa_bwd_group_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
   for (int j = 1; j < group; ++j) acc += src[j * stride4];
   reinterpret_cast<f32x4*>(out)[i4] = acc;
 }
-
-// Wave groups per workgroup: two (the second group takes the other half of
-// every tile, so the grid stays one workgroup per 128 rows and the SIMDs get
-// a second wave to overlap). At D = 128 the dK/dV body then fills the 256
-// VGPRs two waves per SIMD allow (no spill once the copy offsets are
-// recomputed per copy); measured on B4 H16 N4096 causal, two groups beat one
-// (281 VGPRs, one wave per SIMD) by 9%.
-
-template <int D>
-constexpr int kDkdvGroups = 2;
-template <int D>
-constexpr int kDqGroups = 2;
 
 // The three passes (-D_i and -L log2 e, dK/dV, dQ) and, with H_kv < H, the
 // group sums. geo is dense (B heads of N rows per head) or varlen (heads of
@@ -1057,8 +1172,6 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
                      G, lse, nd, nl, rows);
   const int nb = (geo.N + kBlk - 1) / kBlk;
   const int total = (int)(units * nb);
-  constexpr int GK = kDkdvGroups<D>, GQ = kDqGroups<D>;
-  bool launched = false;
   // One launch where it pays (measured): at D = 64 always; at D = 128 for
   // causal heads, where a short wave of workgroups cannot even out the
   // triangle on its own (B1 H8 N4096: 0.237 -> 0.165 ms) and larger grids
@@ -1067,16 +1180,15 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
   // 1082.9 / 1081.2 us; same gradients bit for bit). Non-causal D = 128
   // heads, whose units are all the same length, keep the two launches
   // (B4 H16 N4096: 2.36 vs 2.50 ms).
-  if constexpr (GK == 2 && GQ == 2 && (D == 64 || CAUSAL)) {
+  if constexpr (D == 64 || CAUSAL) {
     hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
                        s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
-    launched = true;
-  }
-  if (!launched) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<D, CAUSAL, GK, BF16>), dim3(total), dim3(256 * GK), 0, s, Q, K,
-                       V, G, nl, nd, dk_q, dv_q, geo, nb, total, c, scale);
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<D, CAUSAL, GQ, BF16>), dim3(total), dim3(256 * GQ), 0, s, Q, K, V,
-                       G, nl, nd, dq, geo, nb, total, c, scale);
+  } else {
+    static_assert(D == 128, "head dimension");
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<CAUSAL, BF16>), dim3(total), dim3(512), 0, s, Q, K, V,
+                       G, nl, nd, dk_q, dv_q, geo, nb, total, c, scale);
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<CAUSAL, BF16>), dim3(total), dim3(512), 0, s, Q, K, V, G,
+                       nl, nd, dq, geo, nb, total, c, scale);
   }
   if (group > 1) {
     // out_heads KV heads of head_rows rows, each the sum of `group`
