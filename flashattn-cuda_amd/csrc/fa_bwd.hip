@@ -18,9 +18,8 @@
 //                       and V: S^T = K Q^T, dP^T = V dO^T, dS^T as above,
 //                       dQ^T += K^T dS^T
 //
-// The two bodies run as one launch (fa_bwd_fused_kernel) at D = 64 and for
-// causal heads at D = 128, as two (fa_bwd_dkdv_kernel, fa_bwd_dq_kernel) for
-// non-causal heads at D = 128. In each workgroup two wave groups take the
+// The two bodies run as one launch (fa_bwd_fused_kernel: a workgroup takes
+// one role by its block index). In each workgroup two wave groups take the
 // two 32-row halves of every tile and run one phase apart, so one wave's
 // MFMAs overlap the other wave's VALU work on every SIMD.
 //
@@ -1065,34 +1064,9 @@ __device__ __forceinline__ void dq_body_pp128(const f16* __restrict__ Q, const f
   if (grp == 0) store_transposed<D>(dQ + head, N, q0 + 32 * qw, lane, acc[0], scale);
 }
 
-// Non-causal D = 128 runs the two bodies as two launches (see launch_bwd).
-template <bool CAUSAL, bool BF16>
-__global__ void __launch_bounds__(512)
-fa_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
-                   const f16* __restrict__ V, const f16* __restrict__ dO,
-                   const float* __restrict__ NL, const float* __restrict__ ND,
-                   float* __restrict__ dK, float* __restrict__ dV, Geom geo, int num_kb,
-                   int total, float c, float scale) {
-  __shared__ __attribute__((aligned(1024))) char smem[dkdv_pp128_smem<128>()];
-  dkdv_body_pp128<128, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dK, dV, geo, num_kb, total, c, scale,
-                                     (int)blockIdx.x, smem);
-}
-
-template <bool CAUSAL, bool BF16>
-__global__ void __launch_bounds__(512)
-fa_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
-                 const f16* __restrict__ V, const f16* __restrict__ dO,
-                 const float* __restrict__ NL, const float* __restrict__ ND,
-                 float* __restrict__ dQ, Geom geo, int num_qb, int total, float c,
-                 float scale) {
-  __shared__ __attribute__((aligned(1024))) char smem[dq_pp128_smem<128>()];
-  dq_body_pp128<128, CAUSAL, BF16>(Q, K, V, dO, NL, ND, dQ, geo, num_qb, total, c, scale,
-                                   (int)blockIdx.x, smem);
-}
-
 // dK/dV and dQ in one launch (both bodies take 8 waves and share one LDS
-// buffer): blocks [0, total) are the dK/dV kernel's, [total, 2 total) the dQ
-// kernel's. Each half is dispatched longest unit first, so a CU that
+// buffer): blocks [0, total) run the dK/dV body, [total, 2 total) the dQ
+// body. Each half is dispatched longest unit first, so a CU that
 // finished a short dK/dV unit (late keys of a causal head) picks up a long
 // dQ unit: the causal triangle's two halves even out across the CUs instead
 // of each kernel waiting for its own longest unit.
@@ -1172,24 +1146,13 @@ static hipError_t launch_bwd(const void* q, const void* k, const void* v, const 
                      G, lse, nd, nl, rows);
   const int nb = (geo.N + kBlk - 1) / kBlk;
   const int total = (int)(units * nb);
-  // One launch where it pays (measured): at D = 64 always; at D = 128 for
-  // causal heads, where a short wave of workgroups cannot even out the
-  // triangle on its own (B1 H8 N4096: 0.237 -> 0.165 ms) and larger grids
-  // run the same in one launch as in two (B2 H8 N4096 303.2 / 301.1 us,
-  // B4 H8 600.8 / 597.2 us, B4 H16 1237.2 / 1237.9 us, B1 H16 N8192
-  // 1082.9 / 1081.2 us; same gradients bit for bit). Non-causal D = 128
-  // heads, whose units are all the same length, keep the two launches
-  // (B4 H16 N4096: 2.36 vs 2.50 ms).
-  if constexpr (D == 64 || CAUSAL) {
-    hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0,
-                       s, Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
-  } else {
-    static_assert(D == 128, "head dimension");
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<CAUSAL, BF16>), dim3(total), dim3(512), 0, s, Q, K, V,
-                       G, nl, nd, dk_q, dv_q, geo, nb, total, c, scale);
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<CAUSAL, BF16>), dim3(total), dim3(512), 0, s, Q, K, V, G,
-                       nl, nd, dq, geo, nb, total, c, scale);
-  }
+  // dK/dV and dQ in one launch. A causal head's short and long units even
+  // out across the CUs (B1 H8 N4096 D128: 0.237 -> 0.165 ms against two
+  // launches); with units of one length the one launch measured level with
+  // two or slightly ahead (D = 128 non-causal, B1 H8 N4096 256.4 -> 254.5 us,
+  // B4 H16 N4096 1981.8 -> 1972.3 us; same gradients bit for bit).
+  hipLaunchKernelGGL((fa_bwd_fused_kernel<D, CAUSAL, BF16>), dim3(2 * total), dim3(512), 0, s,
+                     Q, K, V, G, nl, nd, dk_q, dv_q, dq, geo, nb, total, c, scale);
   if (group > 1) {
     // out_heads KV heads of head_rows rows, each the sum of `group`
     // consecutive query heads' partials

@@ -158,18 +158,19 @@ def test_headline_shape(fa, dev, D, causal):
     np.testing.assert_allclose(dK.sum(axis=2), 0, atol=2e-3 * scale)
 
 
-def test_causal_d128_two_rounds(fa, dev):
-    """D = 128 causal with 512 units per half (B2 H8 N4096): the fused launch
-    over more workgroups than one round of CUs, so units of both roles start
-    as others finish. Two heads against the oracle, every head through the
+@pytest.mark.parametrize("causal", [True, False])
+def test_d128_two_rounds(fa, dev, causal):
+    """D = 128 with 512 units per half (B2 H8 N4096): the fused launch over
+    more workgroups than one round of CUs, so units of both roles start as
+    others finish. Two heads against the oracle, every head through the
     identities of test_headline_shape."""
     B, H, N, D = 2, 8, 4096, 128
     Q, K, V, G = _randn(B, H, N, D, 77)
-    got = _grads(fa, dev, Q, K, V, G, True)
+    got = _grads(fa, dev, Q, K, V, G, causal)
     for b, h in ((0, 0), (B - 1, H - 1)):
         bs, hs = slice(b, b + 1), slice(h, h + 1)
         ref = naive_attention_backward(half_cast(Q[bs, hs]), half_cast(K[bs, hs]),
-                                       half_cast(V[bs, hs]), half_cast(G[bs, hs]), True)
+                                       half_cast(V[bs, hs]), half_cast(G[bs, hs]), causal)
         _compare([g[bs, hs] for g in got], ref, TIGHT_ATOL, TIGHT_RTOL, f"b{b} h{h}")
     dQ, dK, dV = got
     scale = np.sqrt(N)
