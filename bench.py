@@ -239,8 +239,8 @@ def bench_backward(fa, torch, dev, reps=5, iters=20):
     """Backward (dQ, dK, dV from O, L, dO) at the headline shape and at config 3.
 
     TFLOP/s counts the usual 2.5x the forward's products (S, dP, dV, dK, dQ:
-    5 of 2 N^2 D each per head); the three-kernel design recomputes S and dP in
-    the dQ kernel, so it executes 7.
+    5 of 2 N^2 D each per head); the dQ half of the launch recomputes S and dP,
+    so it executes 7.
     """
     res = {}
     for (B, H, N, D, causal) in ((1, 8, 4096, 64, False), (1, 8, 4096, 64, True),
