@@ -1214,7 +1214,7 @@ static int bwd_gqa(bool bf16, const void* q, const void* k, const void* v, const
   if (H_kv <= 0 || H % H_kv != 0) return FA_ERR_KV_HEADS;
   // the partials are written and read as 16-byte vectors
   if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
-  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0, 0, 0};   // nxcd: launcher
   return bf16 ? bwd_run<true>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
                               B * H * N, B * H_kv, N, D, causal, stream)
               : bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
@@ -1257,7 +1257,8 @@ extern "C" int fa_bwd_varlen_f16(const void* q, const void* k, const void* v, co
   if (st != FA_OK) return st;
   if (total == 0) return FA_OK;
   if (H_kv != H && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return FA_ERR_ALIGNMENT;
-  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total, (int)B};
+  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total,
+                       (int)B, 0};   // nxcd: launcher
   return fa::bwd::bwd_run<false>(q, k, v, o, dout, lse, dq, dk, dv, workspace, geo, B * H,
                                  H * total, H_kv, total, D, causal, stream);
 }

@@ -908,7 +908,7 @@ static int fwd_dense(const void* q, const void* k, const void* v, void* o, float
   const int st = fa_validate_fwd_gqa(q, k, v, o, B, H, H_kv, N, D);
   if (st != FA_OK) return st;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
-  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0, 0, 0};   // nxcd: launcher
   return fwd_run(q, k, v, o, lse, geo, B, D, causal, variant, stream);
 }
 }  // namespace fa
@@ -1050,7 +1050,8 @@ extern "C" int fa_fwd_varlen_f16(const void* q, const void* k, const void* v, vo
   const int st = fa_validate_fwd_varlen(q, k, v, o, cu_seqlens, B, H, H_kv, max_seqlen, total, D);
   if (st != FA_OK) return st;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
-  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total, (int)B};
+  const fa::Geom geo{cu_seqlens, (int)max_seqlen, (int)H, (int)(H / H_kv), (int)total,
+                       (int)B, 0};   // nxcd: launcher
   return fa::fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream);
 }
 
@@ -1061,7 +1062,7 @@ extern "C" int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o,
   const int st = fa_validate_fwd_gqa(q, k, v, o, B, H, H_kv, N, D);
   if (st != FA_OK) return st;
   if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3u) != 0) return FA_ERR_ALIGNMENT;
-  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0};
+  const Geom geo{nullptr, (int)N, (int)H, (int)(H / H_kv), 0, 0, 0};   // nxcd: launcher
   // The fp16 path's kernel choice for the shape, with bf16 operands.
   return fwd_run(q, k, v, o, lse, geo, B, D, causal, 0, stream, true);
 }
