@@ -118,10 +118,14 @@ def test_ragged_hot_rows(fa, dev, D):
         print(f"hot rows N{N} D{D} causal={causal}  max diffs dQ/dK/dV {d}")
 
 
-def test_deterministic(fa, dev):
-    Q, K, V, G = _randn(1, 4, 777, 64, 5)
-    a = _grads(fa, dev, Q, K, V, G, False)
-    b = _grads(fa, dev, Q, K, V, G, False)
+@pytest.mark.parametrize("D,causal", [(64, False), (64, True), (128, False), (128, True)])
+def test_deterministic(fa, dev, D, causal):
+    """Bitwise-repeatable gradients (no atomics, fixed reduction orders) from
+    both ping-pong forms, over a ragged length and more units than CUs
+    (B4 H8 N2100: 544 units per half)."""
+    Q, K, V, G = _randn(4, 8, 2100, D, 5)
+    a = _grads(fa, dev, Q, K, V, G, causal)
+    b = _grads(fa, dev, Q, K, V, G, causal)
     for x, y in zip(a, b):
         assert np.array_equal(x, y), "backward must be bitwise reproducible (no atomics)"
 
